@@ -1,0 +1,71 @@
+"""Helpers shared by the GPU parity tests."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from oracle import synth
+
+
+def dev(a) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu()
+    if t.dtype == torch.uint16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    return t.numpy()
+
+
+def rel_err(got, want) -> float:
+    """max |got - want| / max |want| -- the tolerance metric for FP32 outputs."""
+    want = np.asarray(want, np.float64)
+    denom = max(float(np.abs(want).max()), 1e-30)
+    return float(np.abs(np.asarray(got, np.float64) - want).max() / denom)
+
+
+def same_bits(a, b) -> bool:
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    return a.shape == b.shape and a.dtype == b.dtype and np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+_GETTERS = {
+    "S_K": "get_S_K", "S_V": "get_S_V", "RW_K": "get_RW_K", "RW_V": "get_RW_V", "HH_K": "get_HH_K",
+    "HH_V": "get_HH_V", "HH_token_ids": "get_HH_token_ids", "HH_scores": "get_HH_scores", "WR_K": "get_WR_K",
+    "WR_V": "get_WR_V", "WR_token_ids": "get_WR_token_ids", "PBS_K_Packed": "get_PBS_K_Packed",
+    "PBS_K_Scales": "get_PBS_K_Scales", "PBS_K_Zeroes": "get_PBS_K_Zeroes", "PBS_V_Packed": "get_PBS_V_Packed",
+    "PBS_V_Scales": "get_PBS_V_Scales", "PBS_V_Zeroes": "get_PBS_V_Zeroes", "PBS_token_ids": "get_PBS_token_ids",
+    "global_attn_scores": "get_global_attn_scores",
+}
+
+
+def gpu_engine_state(eng) -> dict:
+    """Counters plus flat host copies of every tier buffer, in the layout of
+    oracle.binding.CpuEngine.state()."""
+    st = {"counters": eng.counters()}
+    for name, getter in _GETTERS.items():
+        st[name] = host(getattr(eng, getter)()).reshape(-1)
+    return st
+
+
+def gpu_state_digest(eng) -> str:
+    st = gpu_engine_state(eng)
+    return synth.state_digest(st["counters"], st)
+
+
+def quantize_blocks_gpu(C, K: torch.Tensor, V: torch.Tensor, kgs: int, fp16: bool):
+    """Pack token-major device K/V [nb*kgs, H, D] into the reference PBS layout."""
+    n, H, D = K.shape
+    nb = n // kgs
+    mdt = torch.uint16 if fp16 else torch.float32
+    dt = "fp16" if fp16 else "fp32"
+    KP = torch.empty((nb, kgs // 16, H, D), dtype=torch.int32, device="cuda")
+    KS = torch.empty((nb, H, D), dtype=mdt, device="cuda")
+    KZ = torch.empty((nb, H, D), dtype=mdt, device="cuda")
+    VP = torch.empty((nb * kgs, H, D // 16), dtype=torch.int32, device="cuda")
+    VS = torch.empty((nb * kgs, H, 1), dtype=mdt, device="cuda")
+    VZ = torch.empty((nb * kgs, H, 1), dtype=mdt, device="cuda")
+    C.quantize_k_blocks(K, KP, KS, KZ, nb, H, D, kgs, dt)
+    C.quantize_v_block(V, VP, VS, VZ, H, D, nb * kgs, dt)
+    return KP, KS, KZ, VP, VS, VZ

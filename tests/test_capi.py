@@ -1,0 +1,66 @@
+"""The C-ABI library loads and exports every entry point include/tritiercache_amd.h declares.
+No compute calls: this runs without a GPU."""
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "tritiercache_amd.h")
+LIB = os.path.join(ROOT, "tritiercache_amd", "libtritiercache_amd.so")
+
+
+def declared_symbols():
+    src = open(HEADER).read()
+    return sorted(set(re.findall(r"^TT_API\s+[\w\s\*]*?\b(tt_\w+)\s*\(", src, re.M)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ("tt_fused_attention_decode", "tt_quantize_k_block", "tt_quantize_v_block", "tt_dequantize_k",
+              "tt_dequantize_v", "tt_engine_create", "tt_engine_step", "tt_engine_prefill", "tt_engine_buffer"):
+        assert s in syms
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="native library not built")
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB], capture_output=True, text=True, check=True).stdout
+    exported = set(re.findall(r"\bT\s+(tt_\w+)", out))
+    missing = [s for s in declared_symbols() if s not in exported]
+    assert not missing, missing
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="native library not built")
+def test_python_binding_signatures_cover_header():
+    from tritiercache_amd import _lib
+
+    assert set(declared_symbols()) == set(_lib.EXPORTED_SYMBOLS)
+    lib = _lib.load()
+    for s in declared_symbols():
+        assert hasattr(lib, s)
+    assert lib.tt_version().decode().startswith("tritiercache_amd")
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="native library not built")
+def test_reference_module_surface():
+    """The symbols the reference CLI requires of tri_tier._C (src/tri_tier/cli.py:153-160)."""
+    from tritiercache_amd import _C
+
+    for s in ("TriTierCacheEngine", "fused_attention_decode", "quantize_k_block", "quantize_v_block", "dequantize_k",
+              "dequantize_v"):
+        assert hasattr(_C, s)
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="native library not built")
+def test_errors_without_gpu_are_python_exceptions():
+    import torch
+
+    from tritiercache_amd import _C
+
+    if torch.cuda.is_available():
+        pytest.skip("checks the no-GPU error path")
+    with pytest.raises(RuntimeError):
+        _C.TriTierCacheEngine(4, 4, 64, 128)
+    with pytest.raises(ValueError):
+        _C.fused_attention_decode(0, None, None, -1, None, None, None, None, None, None, None, 0, 4, 4, 64, 0)

@@ -1,0 +1,169 @@
+"""GPU parity of the device-resident engine (tier maintenance + fused step).
+
+* score-injected tier maintenance (ingest + decayed feedback with synthetic
+  weights): the full engine state must equal the compiled reference's, bit for
+  bit, at every checkpoint (digests in tests/golden/engine_digests.json);
+* full steps: the GPU computes attention and mean weights; the oracle engine is
+  fed the GPU's mean weights (score-injected lockstep), so tier membership,
+  packed words, scales/zeros and scores must match bit for bit while the
+  attention outputs match within 1e-4;
+* prefill paths, counters, zero-copy views, byte accounting.
+"""
+import numpy as np
+import pytest
+import torch
+
+import engine_runs
+from oracle import synth
+from gpu_helpers import dev, gpu_engine_state, gpu_state_digest, host, rel_err, same_bits
+
+pytestmark = pytest.mark.gpu
+ATTN_TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def C():
+    assert torch.cuda.is_available(), "GPU test on a machine without a GPU"
+    from tritiercache_amd import _C
+
+    return _C
+
+
+def gpu_engine(C, cfg):
+    Hq, Hkv, D, msl, S, R, hr, decay, iv, kgs, fp16 = engine_runs.engine_args(cfg)
+    return C.TriTierCacheEngine(Hq, Hkv, D, msl, S, R, hr, decay, iv, kgs, "fp16" if fp16 else "fp32")
+
+
+@pytest.mark.parametrize("run", ["inject_maint_fp16", "inject_maint_fp32"])
+def test_tier_maintenance_matches_reference_digests(C, golden, run):
+    """2048 appends at 32 KV heads x 128, ring 256, 4 sinks, 5% heavy hitters."""
+    cfg = engine_runs.RUNS[run]
+    want = golden["engine"][run]
+    eng = gpu_engine(C, cfg)
+    for s in range(cfg["steps"]):
+        _, K, V = engine_runs.step_inputs(cfg, s)
+        eng.ingest(dev(K), dev(V))
+        w = engine_runs.inject_weights(cfg, s, eng.visible())
+        eng.feedback(dev(w))
+        if engine_runs.is_checkpoint(cfg, s):
+            assert gpu_state_digest(eng) == want["digests"][str(s)], (run, s)
+    c = eng.counters()
+    assert all(c[k] == v for k, v in want["final_counters"].items()), (c, want["final_counters"])
+
+
+def _compare_state(g, o, tag):
+    assert g["counters"] == o["counters"], (tag, g["counters"], o["counters"])
+    for name in o:
+        if name == "counters":
+            continue
+        assert same_bits(g[name], o[name].reshape(-1)), (tag, name)
+
+
+@pytest.mark.parametrize("run", ["step_small_fp16", "step_prefill_kgs32_fp32", "step_gqa_d128_fp32"])
+def test_full_steps_lockstep_with_oracle(C, oracle, run):
+    cfg = engine_runs.RUNS[run]
+    eng = gpu_engine(C, cfg)
+    oe = oracle.engine(*engine_runs.engine_args(cfg))
+    if cfg["prefill"]:
+        Kp, Vp = engine_runs.prefill_inputs(cfg)
+        eng.prefill(dev(Kp), dev(Vp), Kp.shape[0])
+        oe.prefill(Kp, Vp)
+        _compare_state(gpu_engine_state(eng), oe.state(), "prefill")
+    for s in range(cfg["steps"]):
+        Q, K, V = engine_runs.step_inputs(cfg, s)
+        out = torch.empty(cfg["Hq"] * cfg["D"], dtype=torch.float32, device="cuda")
+        eng.step(dev(Q), dev(K), dev(V), out)
+        g_mw = host(eng.get_mean_attn_weights())
+        oe.ingest(K, V)
+        ro, rmw = oe.attend(Q)
+        assert rel_err(host(out), ro) <= ATTN_TOL, (run, s)
+        assert rel_err(g_mw, rmw) <= ATTN_TOL, (run, s)
+        oe.feedback(g_mw)
+        if engine_runs.is_checkpoint(cfg, s):
+            _compare_state(gpu_engine_state(eng), oe.state(), (run, s))
+
+
+@pytest.mark.parametrize("q_len", [0, 3, 4, 10, 20, 21, 36, 37, 52, 100, 171])
+@pytest.mark.parametrize("kgs,fp16", [(16, True), (32, False)])
+def test_prefill_vs_oracle(C, oracle, q_len, kgs, fp16):
+    Hq, Hkv, D, msl, S, R = 4, 2, 32, 256, 4, 16
+    eng = C.TriTierCacheEngine(Hq, Hkv, D, msl, S, R, 0.1, 0.999, 16, kgs, "fp16" if fp16 else "fp32")
+    oe = oracle.engine(Hq, Hkv, D, msl, S, R, 0.1, 0.999, 16, kgs, fp16)
+    K = synth.normal(77, q_len, (max(q_len, 1), Hkv, D))[:q_len]
+    V = synth.normal(78, q_len, (max(q_len, 1), Hkv, D))[:q_len]
+    eng.prefill(dev(K) if q_len else torch.empty(0, device="cuda"), dev(V) if q_len else torch.empty(0, device="cuda"),
+                q_len)
+    oe.prefill(K, V, q_len)
+    _compare_state(gpu_engine_state(eng), oe.state(), q_len)
+    # then decode a few steps in lockstep
+    for s in range(40):
+        q = synth.normal(79, s, (Hq * D,))
+        k, v = synth.normal(80, s, (Hkv * D,)), synth.normal(81, s, (Hkv * D,))
+        out = torch.empty(Hq * D, dtype=torch.float32, device="cuda")
+        eng.step(dev(q), dev(k), dev(v), out)
+        g_mw = host(eng.get_mean_attn_weights())
+        oe.ingest(k, v)
+        ro, _ = oe.attend(q)
+        assert rel_err(host(out), ro) <= ATTN_TOL
+        oe.feedback(g_mw)
+    _compare_state(gpu_engine_state(eng), oe.state(), ("after", q_len))
+
+
+def test_engine_properties_and_views(C, oracle):
+    """Attributes and getters of the reference binding (bindings.cpp:437-626)."""
+    eng = C.TriTierCacheEngine(4, 2, 64, 256, 4, 16, 0.1, 0.999, 16, 32, "fp16")
+    assert eng.k_group_size == 32 and eng.chunk_size == 32 and eng.use_fp16_meta is True
+    assert eng.pbs_metadata_dtype == "fp16" and eng.max_hh == 26 and eng.s_count == 0
+    sk = eng.get_S_K()
+    assert sk.shape == (4, 2, 64) and sk.dtype == torch.float32 and sk.is_cuda
+    g = eng.get_global_attn_scores()
+    assert g.shape == (256,) and bool((g == 0).all())
+    assert bool((eng.get_HH_token_ids() == -1).all())
+    K = synth.normal(5, 0, (96, 2, 64))
+    eng.prefill(dev(K), dev(K), 96)
+    assert eng.pbs_count > 0 and eng.pbs_allocated_blocks == 64
+    kp = eng.get_PBS_K_Packed()
+    assert kp.shape == (64, 2, 2, 64) and kp.dtype == torch.int32
+    assert eng.get_PBS_K_Scales().shape == (64, 2, 64) and eng.get_PBS_K_Scales().dtype == torch.uint16
+    assert eng.get_PBS_V_Scales().shape == (64 * 32, 2, 1)
+    # views alias device memory: a step that fills a sink slot shows through an old view
+    eng2 = C.TriTierCacheEngine(4, 2, 64, 256, 4, 16, 0.1, 0.999, 16, 16, "fp32")
+    view = eng2.get_S_K()
+    k = synth.normal(6, 0, (2 * 64,))
+    eng2.step(dev(synth.normal(6, 1, (4 * 64,))), dev(k), dev(k), torch.empty(256, device="cuda"))
+    torch.cuda.synchronize()
+    assert same_bits(host(view[0]).reshape(-1), k)
+
+
+def test_buffer_bytes_matches_oracle(C, oracle):
+    for fp16 in (True, False):
+        eng = C.TriTierCacheEngine(4, 2, 64, 256, 4, 16, 0.1, 0.999, 16, 16, "fp16" if fp16 else "fp32")
+        oe = oracle.engine(4, 2, 64, 256, 4, 16, 0.1, 0.999, 16, 16, fp16)
+        assert eng.get_buffer_bytes() == oe.buffer_bytes()
+        K = synth.normal(9, 0, (96, 2, 64))
+        eng.prefill(dev(K), dev(K), 96)
+        oe.prefill(K, K)
+        assert eng.get_buffer_bytes() == oe.buffer_bytes()
+
+
+def test_reference_wiring_divergence(C):
+    """tests/test_wiring_verification.py:136-182 of the reference on the GPU engine:
+    finite, non-zero outputs that differ between group sizes and metadata types."""
+    rng = np.random.default_rng(999)
+    outs = {}
+    for kgs, dt in ((16, "fp16"), (16, "fp32"), (32, "fp16")):
+        eng = C.TriTierCacheEngine(4, 2, 64, 256, 4, 16, 0.1, 0.999, 16, kgs, dt)
+        rs = np.random.default_rng(999)
+        Kp = rs.standard_normal((96, 2, 64)).astype(np.float32)
+        Vp = rs.standard_normal((96, 2, 64)).astype(np.float32)
+        eng.prefill(Kp, Vp, 96)
+        Q = rs.standard_normal(4 * 64).astype(np.float32)
+        Kn = rs.standard_normal(2 * 64).astype(np.float32)
+        Vn = rs.standard_normal(2 * 64).astype(np.float32)
+        out = np.zeros(4 * 64, np.float32)
+        eng.step(Q, Kn, Vn, out)
+        assert np.all(np.isfinite(out)) and np.any(out != 0)
+        outs[(kgs, dt)] = out
+    assert np.abs(outs[(16, "fp16")] - outs[(32, "fp16")]).max() > 0
+    assert np.abs(outs[(16, "fp16")] - outs[(16, "fp32")]).max() > 0
+    del rng

@@ -1,0 +1,336 @@
+"""GPU parity of the stateless kernels (through the C ABI) against the oracle and the golden fixtures.
+
+Bar: packed words, scales and zeros bit-exact; attention outputs and mean
+weights within max|gpu - ref| / max|ref| <= 1e-4 (FP32, ATTN_TOL below).
+"""
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import synth
+from gpu_helpers import dev, host, quantize_blocks_gpu, rel_err, same_bits
+
+pytestmark = pytest.mark.gpu
+
+ATTN_TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def C():
+    assert torch.cuda.is_available(), "GPU test on a machine without a GPU"
+    from tritiercache_amd import _C
+
+    assert _C.device_count() > 0
+    return _C
+
+
+def _meta(fp16):
+    return (torch.uint16, "fp16") if fp16 else (torch.float32, "fp32")
+
+
+def gpu_quantize_k(C, K, kgs, fp16):
+    kgs_, H, D = K.shape
+    mdt, dt = _meta(fp16)
+    p = torch.zeros((kgs // 16, H, D), dtype=torch.int32, device="cuda")
+    s = torch.zeros((H, D), dtype=mdt, device="cuda")
+    z = torch.zeros((H, D), dtype=mdt, device="cuda")
+    C.quantize_k_block(dev(K), p, s, z, H, D, kgs, dt)
+    return host(p), host(s), host(z)
+
+
+def gpu_quantize_v(C, V, fp16):
+    ch, H, D = V.shape
+    mdt, dt = _meta(fp16)
+    p = torch.zeros((ch, H, D // 16), dtype=torch.int32, device="cuda")
+    s = torch.zeros((ch, H), dtype=mdt, device="cuda")
+    z = torch.zeros((ch, H), dtype=mdt, device="cuda")
+    C.quantize_v_block(dev(V), p, s, z, H, D, ch, dt)
+    return host(p), host(s), host(z)
+
+
+# ------------------------------------------------------------------ quantisers
+def test_quantize_k_golden(C, golden):
+    K = golden["kernels"]
+    for i, c in enumerate(golden["kernels_index"]["qk"]):
+        p, s, z = gpu_quantize_k(C, K[f"qk{i}_K"], c["kgs"], c["fp16"])
+        assert same_bits(p, K[f"qk{i}_packed"]), i
+        assert same_bits(s, K[f"qk{i}_scale"]) and same_bits(z, K[f"qk{i}_zero"]), i
+
+
+def test_quantize_v_golden(C, golden):
+    K = golden["kernels"]
+    for i, c in enumerate(golden["kernels_index"]["qv"]):
+        p, s, z = gpu_quantize_v(C, K[f"qv{i}_V"], c["fp16"])
+        assert same_bits(p, K[f"qv{i}_packed"]), i
+        assert same_bits(s, K[f"qv{i}_scale"]) and same_bits(z, K[f"qv{i}_zero"]), i
+
+
+def test_quantize_v_reference_kat(C, golden):
+    k = golden["qv_kat"]
+    V = np.array(k["V"], np.float32).reshape(16, 2, 32)
+    p, s, z = gpu_quantize_v(C, V, False)
+    assert np.array_equal(p.reshape(-1).view(np.uint32), np.array(k["expected_packed"], np.uint32))
+    assert np.all(np.abs(z.reshape(-1) - np.array(k["expected_min"], np.float32)) <= 1e-4)
+    assert np.all(np.abs(s.reshape(-1) - np.array(k["expected_scale"], np.float32)) <= 1e-4)
+
+
+def test_round_half_even_kat(C, golden):
+    k = golden["tie_kat"]
+    V = np.array(k["V"], np.float32).reshape(16, 1, 16)
+    p, s, z = gpu_quantize_v(C, V, False)
+    assert np.array_equal(p.reshape(-1).view(np.uint32), np.array(k["reference_packed"], np.uint32))
+
+
+def _edge_values(shape, seed):
+    """N(0,1) plus planted edge cases: constant runs, signed zeros, exact ties,
+    huge and tiny magnitudes, fp16 overflow and denormal metadata."""
+    x = synth.normal(seed, 0, shape, std=2.0).reshape(-1)
+    n = x.size
+    x[: n // 16] = 0.5
+    x[n // 16: n // 8: 2] = -0.0
+    x[n // 8: n // 8 + 64] = np.linspace(0, 3, 64, dtype=np.float32)
+    x[n // 4: n // 4 + 32] *= 1e5
+    x[n // 2: n // 2 + 32] *= 1e-6
+    return x.reshape(shape).astype(np.float32)
+
+
+@pytest.mark.parametrize("fp16", [False, True])
+@pytest.mark.parametrize("kgs,H,D", [(16, 1, 8), (16, 3, 12), (16, 8, 128), (32, 4, 64), (16, 32, 128), (32, 2, 256)])
+def test_quantize_k_random_vs_oracle(C, oracle, kgs, H, D, fp16):
+    for seed in range(3):
+        K = _edge_values((kgs, H, D), 1000 + seed)
+        g = gpu_quantize_k(C, K, kgs, fp16)
+        o = oracle.quantize_k(K, kgs, fp16)
+        for a, b in zip(g, o):
+            assert same_bits(a, b), (kgs, H, D, fp16, seed)
+
+
+@pytest.mark.parametrize("fp16", [False, True])
+@pytest.mark.parametrize("ch,H,D", [(16, 1, 16), (16, 8, 128), (32, 4, 64), (16, 32, 128), (16, 2, 256)])
+def test_quantize_v_random_vs_oracle(C, oracle, ch, H, D, fp16):
+    for seed in range(3):
+        V = _edge_values((ch, H, D), 2000 + seed)
+        g = gpu_quantize_v(C, V, fp16)
+        o = oracle.quantize_v(V, fp16)
+        for a, b in zip(g, o):
+            assert same_bits(a, b), (ch, H, D, fp16, seed)
+
+
+@pytest.mark.parametrize("fp16", [False, True])
+def test_dequantize_vs_oracle(C, oracle, fp16):
+    H, D, nb, kgs = 4, 64, 5, 32
+    K = synth.normal(31, 0, (nb * kgs, H, D))
+    mdt, dt = _meta(fp16)
+    packs = [oracle.quantize_k(K[b * kgs:(b + 1) * kgs], kgs, fp16) for b in range(nb)]
+    p, s, z = (np.stack([x[i] for x in packs]) for i in range(3))
+    out = torch.zeros((nb * kgs, H, D), dtype=torch.float32, device="cuda")
+    C.dequantize_k(dev(p), dev(s), dev(z), out, nb, H, D, kgs, dt)
+    assert same_bits(host(out), oracle.dequantize_k(p, s, z, nb, H, D, kgs, fp16))
+    p, s, z = oracle.quantize_v(K, fp16)
+    out = torch.zeros((nb * kgs, H, D), dtype=torch.float32, device="cuda")
+    C.dequantize_v(dev(p), dev(s), dev(z), out, nb * kgs, H, D, dt)
+    assert same_bits(host(out), oracle.dequantize_v(p, s, z, nb * kgs, H, D, fp16))
+
+
+def test_quantize_host_buffers_like_reference_tests(C, oracle):
+    """numpy in / numpy out, as the reference's test_wiring_verification.py calls them."""
+    K = synth.normal(41, 0, (16, 4, 64)) * 2.5 + 1.2345
+    packed = np.zeros((1, 4, 64), np.int32)
+    scale = np.zeros((1, 4, 64), np.uint16)
+    zero = np.zeros((1, 4, 64), np.uint16)
+    C.quantize_k_block(K, packed[0], scale[0], zero[0], 4, 64, 16, "fp16")
+    p, s, z = oracle.quantize_k(K, 16, True)
+    assert same_bits(packed[0], p) and same_bits(scale[0], s) and same_bits(zero[0], z)
+    out = np.zeros((16, 4, 64), np.float32)
+    C.dequantize_k(packed, scale, zero, out, 1, 4, 64, 16, "fp16")
+    assert same_bits(out, oracle.dequantize_k(p, s, z, 1, 4, 64, 16, True))
+
+
+# ---------------------------------------------------------------- fused attention
+def _run_fused_gpu(C, args, want_mw=True):
+    (Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, fp16) = args
+    out = torch.full((Hq, D), float("nan"), dtype=torch.float32, device="cuda")
+    mw = torch.full((nd + nb * kgs,), float("nan"), dtype=torch.float32, device="cuda") if want_mw else None
+    t = lambda a: dev(a) if a is not None and (not hasattr(a, "size") or a.size > 0) else None  # noqa: E731
+    C.fused_attention_decode(dev(Q), t(dK) if nd else None, t(dV) if nd else None, nd,
+                             t(KP) if nb else None, t(KS) if nb else None, t(KZ) if nb else None,
+                             t(VP) if nb else None, t(VS) if nb else None, t(VZ) if nb else None,
+                             t(ids) if nb else None, nb, Hq, Hkv, D, out, mw, kgs, "fp16" if fp16 else "fp32")
+    torch.cuda.synchronize()
+    return host(out), (host(mw) if want_mw else None)
+
+
+def test_fused_attention_golden(C, golden):
+    K = golden["kernels"]
+    for i, c in enumerate(golden["kernels_index"]["fa"]):
+        args = (K[f"fa{i}_Q"], K[f"fa{i}_dK"], K[f"fa{i}_dV"], c["nd"], K[f"fa{i}_KP"], K[f"fa{i}_KS"],
+                K[f"fa{i}_KZ"], K[f"fa{i}_VP"], K[f"fa{i}_VS"], K[f"fa{i}_VZ"], K[f"fa{i}_ids"], c["nb"], c["Hq"],
+                c["Hkv"], c["D"], c["kgs"], c["fp16"])
+        out, mw = _run_fused_gpu(C, args)
+        assert rel_err(out, K[f"fa{i}_out"]) <= ATTN_TOL, i
+        assert rel_err(mw, K[f"fa{i}_mw"]) <= ATTN_TOL, i
+
+
+def make_case(oracle, Hq, Hkv, D, nd, nb, kgs, fp16, mask, seed, k_outliers=False):
+    Q = synth.normal(seed, 0, (Hq, D))
+    dK, dV = synth.normal(seed, 1, (nd, Hkv, D)), synth.normal(seed, 2, (nd, Hkv, D))
+    nbk = max(nb, 1)
+    Kp, Vp = synth.normal(seed, 3, (nbk * kgs, Hkv, D)), synth.normal(seed, 4, (nbk * kgs, Hkv, D))
+    if k_outliers:
+        Kp[:, :, :4] *= 8.0
+        dK[:, :, :4] *= 8.0
+    packs = [(oracle.quantize_k(Kp[b * kgs:(b + 1) * kgs], kgs, fp16), oracle.quantize_v(Vp[b * kgs:(b + 1) * kgs], fp16))
+             for b in range(nbk)]
+    KP = np.stack([k[0] for k, _ in packs])
+    KS = np.stack([k[1] for k, _ in packs])
+    KZ = np.stack([k[2] for k, _ in packs])
+    VP = np.concatenate([v[0] for _, v in packs])
+    VS = np.concatenate([v[1] for _, v in packs])
+    VZ = np.concatenate([v[2] for _, v in packs])
+    ids = np.arange(nbk * kgs, dtype=np.int64) + nd
+    rng = np.random.default_rng(seed)
+    if mask == "tail":
+        ids[-(kgs // 2 + 3):] = -1
+    elif mask == "holes":
+        ids[rng.random(ids.size) < 0.2] = -1
+    elif mask == "block":
+        ids[:kgs] = -1
+    elif mask == "all":
+        ids[:] = -1
+    return (Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, fp16)
+
+
+SWEEP = [
+    # Hq, Hkv, D, nd, nb, kgs, fp16, mask
+    (1, 1, 16, 1, 1, 16, False, "none"),
+    (4, 4, 16, 3, 2, 32, True, "tail"),
+    (8, 2, 32, 17, 5, 16, False, "holes"),
+    (6, 2, 32, 33, 5, 16, True, "block"),
+    (32, 8, 128, 260, 20, 16, False, "none"),
+    (32, 8, 128, 0, 40, 16, True, "tail"),
+    (32, 8, 128, 300, 0, 16, False, "none"),
+    (28, 4, 128, 70, 33, 16, False, "holes"),
+    (12, 1, 64, 5, 9, 32, False, "tail"),
+    (16, 1, 64, 40, 12, 16, True, "none"),
+    (24, 2, 128, 9, 7, 16, False, "block"),
+    (4, 2, 256, 18, 4, 16, True, "holes"),
+    (8, 8, 256, 3, 3, 32, False, "none"),
+    (3, 3, 64, 64, 8, 16, False, "all"),
+]
+
+
+@pytest.mark.parametrize("case", SWEEP, ids=[str(c) for c in SWEEP])
+def test_fused_attention_vs_oracle(C, oracle, case):
+    Hq, Hkv, D, nd, nb, kgs, fp16, mask = case
+    args = make_case(oracle, Hq, Hkv, D, nd, nb, kgs, fp16, mask, seed=500 + SWEEP.index(case))
+    out, mw = _run_fused_gpu(C, args)
+    ro, rmw = oracle.fused_attention_decode(*args)
+    if mask == "all" and nd == 0:
+        assert np.all(out == 0) and np.all(mw == 0)
+        return
+    assert rel_err(out, ro) <= ATTN_TOL, case
+    assert rel_err(mw, rmw) <= ATTN_TOL, case
+    ids = args[10]
+    if nb:
+        assert np.all(mw[nd:][ids[: nb * kgs] == -1] == 0)
+
+
+def test_fused_attention_without_mean_weights(C, oracle):
+    args = make_case(oracle, 32, 8, 128, 100, 30, 16, False, "tail", seed=5)
+    out, _ = _run_fused_gpu(C, args, want_mw=False)
+    ro, _ = oracle.fused_attention_decode(*args)
+    assert rel_err(out, ro) <= ATTN_TOL
+
+
+def test_fused_attention_empty(C, oracle):
+    """dense_count = 0 and num_blocks = 0: output is all zeros (sum_exp guard)."""
+    args = make_case(oracle, 4, 2, 64, 0, 0, 16, False, "none", seed=6)
+    out, mw = _run_fused_gpu(C, args)
+    assert np.all(out == 0)
+
+
+def test_fused_attention_host_pointers_like_reference_benchmark(C, oracle):
+    """CPU tensors passed as data_ptr() integers, as benchmark_latency.py:214-233 does."""
+    args = make_case(oracle, 32, 8, 128, 260, 20, 16, False, "none", seed=7)
+    (Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, fp16) = args
+    ts = [torch.from_numpy(np.ascontiguousarray(a)) for a in (Q, dK, dV, KP, KS, KZ, VP, VS, VZ, ids)]
+    out = torch.empty((Hq, D), dtype=torch.float32)
+    mw = torch.empty((nd + nb * kgs,), dtype=torch.float32)
+    C.fused_attention_decode(ts[0].data_ptr(), ts[1].data_ptr(), ts[2].data_ptr(), nd, ts[3].data_ptr(),
+                             ts[4].data_ptr(), ts[5].data_ptr(), ts[6].data_ptr(), ts[7].data_ptr(), ts[8].data_ptr(),
+                             ts[9].data_ptr(), nb, Hq, Hkv, D, out.data_ptr(), mw.data_ptr())
+    ro, rmw = oracle.fused_attention_decode(*args)
+    assert rel_err(out.numpy(), ro) <= ATTN_TOL and rel_err(mw.numpy(), rmw) <= ATTN_TOL
+
+
+def test_fused_attention_errors(C):
+    z = torch.zeros(16, device="cuda")
+    with pytest.raises(ValueError):
+        C.fused_attention_decode(z, None, None, -1, None, None, None, None, None, None, None, 0, 1, 1, 16, z)
+    with pytest.raises(ValueError):
+        C.fused_attention_decode(z, None, None, 0, None, None, None, None, None, None, None, -2, 1, 1, 16, z)
+    with pytest.raises(ValueError):
+        C.fused_attention_decode(z, None, None, 0, None, None, None, None, None, None, None, 0, 0, 1, 16, z)
+    with pytest.raises(ValueError):  # GQA ratio must be integral
+        C.fused_attention_decode(z, None, None, 0, None, None, None, None, None, None, None, 0, 3, 2, 16, z)
+    with pytest.raises(ValueError):  # unsupported head_dim
+        C.fused_attention_decode(z, None, None, 0, None, None, None, None, None, None, None, 0, 1, 1, 24, z)
+    with pytest.raises(ValueError):  # dense tier missing while dense_count > 0
+        C.fused_attention_decode(z, None, None, 3, None, None, None, None, None, None, None, 0, 1, 1, 16, z)
+    with pytest.raises(ValueError):
+        C.fused_attention_decode(torch.zeros(4, 4, device="cuda").t(), None, None, 0, None, None, None, None, None,
+                                 None, None, 0, 1, 1, 16, z)
+
+
+# ------------------------------------------------------- full-size single layers
+def _tiered_layer(C, Hq, Hkv, D, ctx, fp16, seed, k_outliers=False, student_t=False):
+    """One layer at full context: 4 sinks + 256 recent + ceil(5%) heavy hitters in FP32,
+    the rest packed on the GPU in 16-token blocks; the last block padded with a copy
+    of the last valid token and -1 ids. Returns device tensors and host copies."""
+    S, R = 4, 256
+    hh = int(np.ceil(np.float32(ctx) * np.float32(0.05)))
+    nd = S + hh + R
+    npk = ctx - nd
+    nb = (npk + 15) // 16
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    K = torch.randn((ctx, Hkv, D), generator=g, device="cuda")
+    V = torch.randn((ctx, Hkv, D), generator=g, device="cuda")
+    if k_outliers:
+        ch = torch.randperm(D, generator=g, device="cuda")[:4]
+        K[:, :, ch] *= 8.0
+    Q = torch.randn((Hq, D), generator=g, device="cuda")
+    dK, dV = K[:nd].contiguous(), V[:nd].contiguous()
+    pk, pv = K[nd:], V[nd:]
+    pad = nb * 16 - npk
+    if pad:
+        pk = torch.cat([pk, pk[-1:].expand(pad, Hkv, D)])
+        pv = torch.cat([pv, pv[-1:].expand(pad, Hkv, D)])
+    blocks = quantize_blocks_gpu(C, pk.contiguous(), pv.contiguous(), 16, fp16)
+    ids = torch.arange(nb * 16, dtype=torch.int64, device="cuda") + nd
+    if pad:
+        ids[-pad:] = -1
+    return Q, dK, dV, nd, blocks, ids, nb
+
+
+@pytest.mark.parametrize("name,Hq,Hkv,ctx,fp16", [
+    ("mha-8k", 32, 32, 8192, False),
+    ("llama3-8b-32k", 32, 8, 32768, False),
+    ("llama3-8b-32k-fp16", 32, 8, 32768, True),
+])
+def test_full_size_layer_vs_oracle(C, oracle, name, Hq, Hkv, ctx, fp16):
+    D = 128
+    Q, dK, dV, nd, blocks, ids, nb = _tiered_layer(C, Hq, Hkv, D, ctx, fp16, seed=ctx + Hkv,
+                                                   k_outliers=(Hkv == 8))
+    out = torch.empty((Hq, D), dtype=torch.float32, device="cuda")
+    mw = torch.empty((nd + nb * 16,), dtype=torch.float32, device="cuda")
+    dt = "fp16" if fp16 else "fp32"
+    C.fused_attention_decode(Q, dK, dV, nd, *blocks, ids, nb, Hq, Hkv, D, out, mw, 16, dt)
+    torch.cuda.synchronize()
+    hb = [host(b) for b in blocks]
+    ro, rmw = oracle.fused_attention_decode(host(Q), host(dK), host(dV), nd, *hb, host(ids), nb, Hq, Hkv, D, 16,
+                                            fp16)
+    assert rel_err(host(out), ro) <= ATTN_TOL, name
+    assert rel_err(host(mw), rmw) <= ATTN_TOL, name
+    assert abs(float(host(mw).astype(np.float64).sum()) - 1.0) < 1e-3

@@ -1,0 +1,201 @@
+"""Pins the oracle (oracle/tt_oracle.c) before it is trusted as the checker.
+
+* the reference's own known-answer vectors (tests/test_quantize_v.cpp,
+  tests/tie_test_v.cpp), via tests/golden/*.json;
+* fixtures written by the compiled reference (tests/golden/make_golden.py):
+  kernel outputs and engine state digests, bit for bit;
+* what the mathematics fixes: dequantisation error bounds, field layout under
+  permutation, float64 softmax attention, mean weights summing to one.
+"""
+import numpy as np
+import pytest
+
+from oracle import synth
+import engine_runs
+
+
+def same_bits(a, b):
+    a, b = np.ascontiguousarray(a), np.ascontiguousarray(b)
+    return a.shape == b.shape and a.dtype == b.dtype and np.array_equal(a.view(np.uint8), b.view(np.uint8))
+
+
+# ---------------------------------------------------------------- reference KATs
+def test_quantize_v_reference_kat(oracle, golden):
+    k = golden["qv_kat"]
+    V = np.array(k["V"], np.float32).reshape(k["chunk_size"], k["num_heads"], k["head_dim"])
+    p, s, z = oracle.quantize_v(V, fp16=False)
+    assert np.all(np.abs(z.reshape(-1) - np.array(k["expected_min"], np.float32)) <= k["tolerance_min_scale"])
+    assert np.all(np.abs(s.reshape(-1) - np.array(k["expected_scale"], np.float32)) <= k["tolerance_min_scale"])
+    assert np.array_equal(p.reshape(-1).view(np.uint32), np.array(k["expected_packed"], np.uint32))
+    # one (token, head) row is constant -1.5: the 1e-9 scale floor and all-zero words
+    row = int(np.flatnonzero(np.array(k["expected_min"], np.float32) == np.float32(-1.5))[0])
+    assert s.reshape(-1)[row] == np.float32(1e-9)
+    assert np.all(p.reshape(-1, 2)[row] == 0)
+
+
+def test_round_half_even_kat(oracle, golden):
+    k = golden["tie_kat"]
+    V = np.array(k["V"], np.float32).reshape(16, 1, 16)
+    p, s, z = oracle.quantize_v(V, fp16=False)
+    w = int(p.reshape(-1).view(np.uint32)[0])
+    for ch, want in k["expected_q"].items():
+        assert (w >> (2 * int(ch))) & 3 == want
+    assert s[0, 0] == k["expected_scale0"]
+    assert np.array_equal(p.reshape(-1).view(np.uint32), np.array(k["reference_packed"], np.uint32))
+
+
+# ------------------------------------------------------- compiled-reference fixtures
+def test_quantize_k_fixtures(oracle, golden):
+    K = golden["kernels"]
+    for i, c in enumerate(golden["kernels_index"]["qk"]):
+        p, s, z = oracle.quantize_k(K[f"qk{i}_K"], c["kgs"], c["fp16"])
+        assert same_bits(p, K[f"qk{i}_packed"]), i
+        assert same_bits(s, K[f"qk{i}_scale"]) and same_bits(z, K[f"qk{i}_zero"]), i
+        d = oracle.dequantize_k(p, s, z, 1, c["H"], c["D"], c["kgs"], c["fp16"])
+        assert same_bits(d, K[f"qk{i}_deq"]), i
+
+
+def test_quantize_v_fixtures(oracle, golden):
+    K = golden["kernels"]
+    for i, c in enumerate(golden["kernels_index"]["qv"]):
+        p, s, z = oracle.quantize_v(K[f"qv{i}_V"], c["fp16"])
+        assert same_bits(p, K[f"qv{i}_packed"]), i
+        assert same_bits(s, K[f"qv{i}_scale"]) and same_bits(z, K[f"qv{i}_zero"]), i
+        d = oracle.dequantize_v(p, s, z, c["chunk"], c["H"], c["D"], c["fp16"])
+        assert same_bits(d, K[f"qv{i}_deq"]), i
+
+
+def _fa_args(K, i, c):
+    return (K[f"fa{i}_Q"], K[f"fa{i}_dK"], K[f"fa{i}_dV"], c["nd"], K[f"fa{i}_KP"], K[f"fa{i}_KS"], K[f"fa{i}_KZ"],
+            K[f"fa{i}_VP"], K[f"fa{i}_VS"], K[f"fa{i}_VZ"], K[f"fa{i}_ids"], c["nb"], c["Hq"], c["Hkv"], c["D"],
+            c["kgs"], c["fp16"])
+
+
+def test_fused_attention_fixtures(oracle, golden):
+    """Same glibc expf, same summation order as the AVX2 kernel: bit-exact on this host."""
+    K = golden["kernels"]
+    for i, c in enumerate(golden["kernels_index"]["fa"]):
+        out, mw = oracle.fused_attention_decode(*_fa_args(K, i, c))
+        np.testing.assert_allclose(out, K[f"fa{i}_out"], rtol=0, atol=2e-6 * max(1.0, np.abs(out).max()))
+        np.testing.assert_allclose(mw, K[f"fa{i}_mw"], rtol=0, atol=1e-7)
+
+
+# ------------------------------------------------------------ closed-form checks
+@pytest.mark.parametrize("fp16", [False, True])
+@pytest.mark.parametrize("kgs", [16, 32])
+def test_quantize_k_error_bound_and_layout(oracle, kgs, fp16):
+    """Each dequantised value lies within half a quantisation step of the input,
+    and permuting the tokens of a block permutes their 2-bit fields."""
+    H, D = 3, 32
+    K = synth.normal(7, kgs, (kgs, H, D), std=2.0)
+    p, s, z = oracle.quantize_k(K, kgs, fp16)
+    d = oracle.dequantize_k(p, s, z, 1, H, D, kgs, fp16)
+    sf = (s.view(np.float16).astype(np.float32) if fp16 else s)[None]
+    zf = (z.view(np.float16).astype(np.float32) if fp16 else z)[None]
+    # half-step rounding, plus the binary16 rounding of scale and zero (2^-11 relative each)
+    bound = sf * 0.5 + 1e-6 + ((3 * sf + np.abs(zf)) * 2.0 ** -10 if fp16 else 0)
+    assert np.all(np.abs(d - K) <= bound)
+    perm = np.random.default_rng(0).permutation(kgs)
+    p2, s2, z2 = oracle.quantize_k(K[perm], kgs, fp16)
+    assert same_bits(s2, s) and same_bits(z2, z)
+    f1 = np.stack([(p.reshape(kgs // 16, H, D)[t // 16].view(np.uint32) >> (2 * (t % 16))) & 3 for t in range(kgs)])
+    f2 = np.stack([(p2.reshape(kgs // 16, H, D)[t // 16].view(np.uint32) >> (2 * (t % 16))) & 3 for t in range(kgs)])
+    assert np.array_equal(f2, f1[perm])
+
+
+def test_quantize_v_error_bound_and_layout(oracle):
+    H, D = 2, 64
+    V = synth.normal(8, 0, (16, H, D), std=1.5)
+    p, s, z = oracle.quantize_v(V, fp16=False)
+    d = oracle.dequantize_v(p, s, z, 16, H, D, False)
+    assert np.all(np.abs(d - V) <= s[:, :, None] * 0.5 + 1e-6)
+    perm = np.random.default_rng(1).permutation(D)
+    p2, s2, z2 = oracle.quantize_v(V[:, :, perm], fp16=False)
+    assert same_bits(s2, s) and same_bits(z2, z)
+
+    def fields(pk):
+        w = pk.view(np.uint32)
+        return np.stack([(w[:, :, c // 16] >> (2 * (c % 16))) & 3 for c in range(D)], axis=-1)
+
+    assert np.array_equal(fields(p2), fields(p)[:, :, perm])
+
+
+def test_f16_conversion_against_numpy(oracle):
+    """RNE float -> half against numpy's IEEE conversion (normals, denormals, overflow)."""
+    xs = np.concatenate([synth.normal(9, 0, (4000,), std=1e3), synth.normal(9, 1, (4000,), std=1e-5),
+                         np.array([65504.0, 65519.0, 65520.0, 6.1e-5, 5.96e-8, 2.98e-8, -0.0, 1e-9], np.float32)])
+    import ctypes as C
+
+    f = oracle.lib.orc_f32_to_f16
+    f.argtypes = [C.c_float]
+    f.restype = C.c_uint16
+    got = np.array([f(float(x)) for x in xs], np.uint16)
+    want = xs.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+
+
+def _f64_attention(Q, dK, dV, nd, deqK, deqV, ids, Hq, Hkv, D):
+    G = Hq // Hkv
+    K = np.concatenate([dK, deqK]).astype(np.float64)
+    V = np.concatenate([dV, deqV]).astype(np.float64)
+    valid = np.concatenate([np.ones(nd, bool), ids != -1])
+    out = np.zeros((Hq, D))
+    w = np.zeros((Hq, K.shape[0]))
+    for h in range(Hq):
+        s = K[:, h // G, :] @ Q[h].astype(np.float64) / np.sqrt(D)
+        s[~valid] = -np.inf
+        e = np.exp(s - s.max())
+        w[h] = e / e.sum()
+        out[h] = w[h] @ V[:, h // G, :]
+    return out, w.mean(axis=0)
+
+
+def test_fused_attention_float64_brute_force(oracle):
+    """Softmax attention over the dequantised tiers, in float64, within 1e-5."""
+    Hq, Hkv, D, nd, nb, kgs = 8, 2, 64, 37, 6, 16
+    Q = synth.normal(21, 0, (Hq, D))
+    dK, dV = synth.normal(21, 1, (nd, Hkv, D)), synth.normal(21, 2, (nd, Hkv, D))
+    Kp, Vp = synth.normal(21, 3, (nb * kgs, Hkv, D)), synth.normal(21, 4, (nb * kgs, Hkv, D))
+    blocks = [[], [], [], [], [], []]
+    for b in range(nb):
+        for j, x in enumerate(oracle.quantize_k(Kp[b * kgs:(b + 1) * kgs], kgs, False)):
+            blocks[j].append(x)
+        for j, x in enumerate(oracle.quantize_v(Vp[b * kgs:(b + 1) * kgs], False)):
+            blocks[3 + j].append(x)
+    KP, KS, KZ = (np.stack(x) for x in blocks[:3])
+    VP, VS, VZ = (np.concatenate(x) for x in blocks[3:])
+    ids = np.arange(nb * kgs, dtype=np.int64)
+    ids[-5:] = -1
+    out, mw = oracle.fused_attention_decode(Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, False)
+    deqK = oracle.dequantize_k(KP, KS, KZ, nb, Hkv, D, kgs, False)
+    deqV = oracle.dequantize_v(VP, VS, VZ, nb * kgs, Hkv, D, False)
+    ref_out, ref_mw = _f64_attention(Q, dK, dV, nd, deqK, deqV, ids, Hq, Hkv, D)
+    assert np.abs(out - ref_out).max() <= 1e-5 * np.abs(ref_out).max()
+    assert np.abs(mw - ref_mw).max() <= 1e-6
+    assert abs(float(mw.sum(dtype=np.float64)) - 1.0) < 1e-5
+    assert np.all(mw[nd + nb * kgs - 5:] == 0)
+
+
+# ---------------------------------------------------------------- engine digests
+@pytest.mark.parametrize("run", sorted(engine_runs.RUNS))
+def test_engine_matches_reference_digests(oracle, golden, run):
+    """The oracle engine reproduces the compiled reference engine's full state
+    (counters, tier buffers, packed store, global scores) bit for bit at every
+    checkpoint, in full-step mode (reference attention included) and in
+    score-injected tier-maintenance mode."""
+    cfg = engine_runs.RUNS[run]
+    want = golden["engine"][run]
+    e = oracle.engine(*engine_runs.engine_args(cfg))
+    if cfg["prefill"]:
+        e.prefill(*engine_runs.prefill_inputs(cfg))
+    for s in range(cfg["steps"]):
+        Q, K, V = engine_runs.step_inputs(cfg, s)
+        if cfg["mode"] == "step":
+            e.step(Q, K, V)
+        else:
+            e.ingest(K, V)
+            e.feedback(engine_runs.inject_weights(cfg, s, e.visible()))
+        if engine_runs.is_checkpoint(cfg, s):
+            st = e.state()
+            assert synth.state_digest(st["counters"], st) == want["digests"][str(s)], (run, s)
+    assert e.counters() == want["final_counters"]

@@ -1,0 +1,83 @@
+// tt_attn.h -- host interface of the fused decode attention kernels.
+#pragma once
+#include "tt_common.h"
+
+namespace tt {
+
+// Engine counters kept in device memory (int32 slots; the threshold is a
+// float stored in slot kThreshold). Kernels index this array directly.
+enum StateSlot : int {
+    kSCount = 0,
+    kRwCount = 1,
+    kRwHead = 2,
+    kHhCount = 3,
+    kWrCount = 4,
+    kBlocksUsed = 5,
+    kPbsCount = 6,
+    kTotal = 7,
+    kLastCalcPos = 8,
+    kTotalEvictions = 9,
+    kLogicalAlloc = 10,
+    kThreshold = 11,
+    kStateSlots = 16,
+};
+
+// Where the attended tokens live. Dense tokens are, in logical order,
+// seg0 rows [0, n0), seg1 rows [0, n1), then seg2 read as a ring of
+// `ring_size` rows starting at `ring_head` for n2 rows. Rows are
+// [num_kv_heads, head_dim] f32. For the stateless entry point seg0 is the
+// caller's dense_K/V and n1 = n2 = 0. When `state` is set (engine), n0/n1/n2,
+// ring_head and num_blocks are read from device memory instead.
+struct AttnInputs {
+    const float* Q = nullptr;
+    const float* k0 = nullptr; const float* v0 = nullptr;
+    const float* k1 = nullptr; const float* v1 = nullptr;
+    const float* k2 = nullptr; const float* v2 = nullptr;
+    int n0 = 0, n1 = 0, n2 = 0;
+    int ring_size = 1, ring_head = 0;
+    const int* state = nullptr;
+    const int32_t* kp = nullptr; const void* ks = nullptr; const void* kz = nullptr;
+    const int32_t* vp = nullptr; const void* vs = nullptr; const void* vz = nullptr;
+    const int64_t* ids = nullptr;
+    int num_blocks = 0;
+    int Hq = 0, Hkv = 0, D = 0, kgs = 16;
+    int meta_fp16 = 0;
+};
+
+// Score feedback applied by the mean-weight kernel (engine only):
+// g[tid] = fmaf(decay, g[tid], mw[i]) for every visible token i, and
+// HH_scores[slot] = g[tid] for heavy-hitter slots (cache_engine.cpp:511-540).
+struct Feedback {
+    float* g = nullptr;
+    float* hh_scores = nullptr;
+    const int64_t* hh_ids = nullptr;
+    const int64_t* pbs_ids = nullptr;
+    int max_seq_len = 0;
+    float decay = 1.0f;
+};
+
+struct AttnPlan {
+    int nsplit = 1;
+    int ld = 0;          // logits row stride (floats)
+    int token_ub = 0;    // upper bound on attended tokens
+    size_t off_ml = 0, off_acc = 0, off_rowstat = 0, off_logits = 0, bytes = 0;
+    bool logits = false;
+};
+
+// Plans the split-K launch for an upper bound of dense tokens / blocks.
+AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs, bool need_logits);
+
+// Enqueues split + merge (+ mean weights / feedback / per-head weights).
+// mean_w: [token count] or null; head_w: [Hq, head_w_ld] or null.
+int attn_launch(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out, float* mean_w,
+                const Feedback* fb, float* head_w, int head_w_ld, hipStream_t stream);
+// The two phases of attn_launch: per-split partials (+ logits) into `ws`,
+// then the merge / mean weights / feedback that read them.
+int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipStream_t stream);
+int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out, float* mean_w,
+                         const Feedback* fb, float* head_w, int head_w_ld, hipStream_t stream);
+
+// Validates shapes the kernels support.
+int attn_check_shapes(int Hq, int Hkv, int D, int kgs);
+
+}  // namespace tt

@@ -1,0 +1,253 @@
+// tt_capi.hip -- extern "C" entry points for the stateless kernels, error
+// reporting and device queries. The engine's entry points are in tt_engine.hip.
+//
+// Argument validation follows the reference binding (csrc/bindings.cpp:120-128,
+// 139-147: counts non-negative, heads/dim positive, data pointers nullable
+// exactly when their count is zero) and adds the shape limits of the gfx950
+// kernels (GQA ratio integral, head_dim a power of two in [16, 256]).
+#include "tt_attn.h"
+
+#include <mutex>
+#include <unordered_map>
+
+namespace tt {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string& msg) { g_last_error = msg; }
+void clear_error() { g_last_error.clear(); }
+
+namespace {
+
+// Library-owned attention workspace, one per device, grown on demand.
+struct DeviceWorkspace {
+    void* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::unordered_map<int, DeviceWorkspace> g_ws;
+
+int get_workspace(size_t bytes, void** out) {
+    int dev = 0;
+    TT_HIP_CHECK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    DeviceWorkspace& w = g_ws[dev];
+    if (w.bytes < bytes) {
+        if (w.ptr) {
+            TT_HIP_CHECK(hipDeviceSynchronize());
+            TT_HIP_CHECK(hipFree(w.ptr));
+            w.ptr = nullptr;
+            w.bytes = 0;
+        }
+        const size_t nb = std::max(bytes, static_cast<size_t>(1) << 20);
+        TT_HIP_CHECK(hipMalloc(&w.ptr, nb));
+        w.bytes = nb;
+    }
+    *out = w.ptr;
+    return TT_OK;
+}
+
+int check_common(int dense_count, int num_blocks, int Hq, int Hkv, int D, int kgs) {
+    if (dense_count < 0) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "dense_count must be non-negative.");
+    if (num_blocks < 0) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_blocks must be non-negative.");
+    return attn_check_shapes(Hq, Hkv, D, kgs);
+}
+
+// Validates the stateless attention arguments and fills the kernel inputs and plan.
+int prepare(const float* Q, const float* dK, const float* dV, int dense_count, const int32_t* KP, const void* KS,
+            const void* KZ, const int32_t* VP, const void* VS, const void* VZ, const int64_t* ids, int num_blocks,
+            int Hq, int Hkv, int D, int kgs, int meta_fp16, bool want_mw, AttnInputs* in, AttnPlan* plan) {
+    int rc = check_common(dense_count, num_blocks, Hq, Hkv, D, kgs);
+    if (rc) return rc;
+    if (!Q) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'Q' pointer address is NULL.");
+    if (dense_count > 0 && (!dK || !dV))
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'dense_K'/'dense_V' pointer address is NULL.");
+    if (num_blocks > 0 && (!KP || !KS || !KZ || !VP || !VS || !VZ || !ids))
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "PBS arguments must be non-NULL when num_blocks > 0.");
+    *plan = attn_plan(dense_count, num_blocks, Hq, Hkv, D, kgs, want_mw);
+    in->Q = Q;
+    in->k0 = dK;
+    in->v0 = dV;
+    in->n0 = dense_count;
+    in->kp = KP;
+    in->ks = KS;
+    in->kz = KZ;
+    in->vp = VP;
+    in->vs = VS;
+    in->vz = VZ;
+    in->ids = ids;
+    in->num_blocks = num_blocks;
+    in->Hq = Hq;
+    in->Hkv = Hkv;
+    in->D = D;
+    in->kgs = kgs;
+    in->meta_fp16 = meta_fp16 ? 1 : 0;
+    return TT_OK;
+}
+
+enum Phase { kBoth, kPartials, kFinalize };
+
+int fused_impl(const float* Q, const float* dK, const float* dV, int dense_count, const int32_t* KP, const void* KS,
+               const void* KZ, const int32_t* VP, const void* VS, const void* VZ, const int64_t* ids, int num_blocks,
+               int Hq, int Hkv, int D, float* out, float* mw, int kgs, int meta_fp16, void* ws, size_t ws_bytes,
+               bool own_ws, Phase phase, int want_mw, hipStream_t s) {
+    AttnInputs in;
+    AttnPlan plan;
+    const bool logits = (phase == kBoth) ? (mw != nullptr) : (want_mw != 0);
+    int rc = prepare(Q, dK, dV, dense_count, KP, KS, KZ, VP, VS, VZ, ids, num_blocks, Hq, Hkv, D, kgs, meta_fp16,
+                     logits, &in, &plan);
+    if (rc) return rc;
+    if (phase != kPartials && !out) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'attn_output' pointer address is NULL.");
+    if (phase == kFinalize && mw && !logits)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "mean_attn_weights requested but the partials were planned without them.");
+    if (own_ws) {
+        rc = get_workspace(plan.bytes, &ws);
+        if (rc) return rc;
+    } else if (!ws || ws_bytes < plan.bytes) {
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "workspace is NULL or smaller than tt_fused_attention_workspace_bytes().");
+    }
+    if (phase == kPartials) return attn_launch_split(in, plan, ws, s);
+    if (phase == kFinalize) return attn_launch_finalize(in, plan, ws, out, mw, nullptr, nullptr, 0, s);
+    return attn_launch(in, plan, ws, out, mw, nullptr, nullptr, 0, s);
+}
+
+}  // namespace
+}  // namespace tt
+
+using namespace tt;
+
+extern "C" {
+
+const char* tt_last_error(void) { return g_last_error.c_str(); }
+
+const char* tt_version(void) { return "tritiercache_amd 0.1.0 gfx950"; }
+
+int tt_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n;
+}
+
+int tt_pointer_kind(const void* ptr) {
+    if (!ptr) return 0;
+    hipPointerAttribute_t attr;
+    if (hipPointerGetAttributes(&attr, ptr) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    if (attr.type == hipMemoryTypeDevice || attr.type == hipMemoryTypeManaged) return 1;
+    if (attr.type == hipMemoryTypeHost) return 2;
+    return 0;
+}
+
+int tt_quantize_k_block(const float* K, uint32_t* packed, void* scale, void* zero, int num_blocks, int num_heads,
+                        int head_dim, int k_group_size, int meta_fp16, void* stream) {
+    clear_error();
+    if (num_blocks < 0 || num_heads <= 0 || head_dim <= 0)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_blocks must be >= 0; num_heads and head_dim must be positive.");
+    if (k_group_size != 16 && k_group_size != 32) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "k_group_size must be 16 or 32.");
+    if (!K || !packed || !scale || !zero) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "quantize_k_block: NULL pointer argument.");
+    return launch_quantize_k(K, packed, scale, zero, num_blocks, num_heads, head_dim, k_group_size, meta_fp16, nullptr,
+                             as_stream(stream));
+}
+
+int tt_quantize_v_block(const float* V, int32_t* packed, void* scale, void* zero, int tokens, int num_heads,
+                        int head_dim, int meta_fp16, void* stream) {
+    clear_error();
+    if (tokens < 0 || num_heads <= 0 || head_dim <= 0)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "tokens must be >= 0; num_heads and head_dim must be positive.");
+    if (head_dim % 16 != 0) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "quantize_v_block: head_dim must be a multiple of 16.");
+    if (!V || !packed || !scale || !zero) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "quantize_v_block: NULL pointer argument.");
+    return launch_quantize_v(V, packed, scale, zero, tokens, num_heads, head_dim, meta_fp16, nullptr, 0,
+                             as_stream(stream));
+}
+
+int tt_dequantize_k(const int32_t* packed, const void* scale, const void* zero, float* out, int num_blocks,
+                    int num_heads, int head_dim, int k_group_size, int meta_fp16, void* stream) {
+    clear_error();
+    if (num_blocks < 0 || num_heads <= 0 || head_dim <= 0)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_blocks must be >= 0; num_heads and head_dim must be positive.");
+    if (k_group_size != 16 && k_group_size != 32) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "k_group_size must be 16 or 32.");
+    if (num_blocks > 0 && (!packed || !scale || !zero || !out))
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "dequantize_k: NULL pointer argument.");
+    return launch_dequantize_k(packed, scale, zero, out, num_blocks, num_heads, head_dim, k_group_size, meta_fp16,
+                               as_stream(stream));
+}
+
+int tt_dequantize_v(const int32_t* packed, const void* scale, const void* zero, float* out, int total_tokens,
+                    int num_heads, int head_dim, int meta_fp16, void* stream) {
+    clear_error();
+    if (total_tokens < 0 || num_heads <= 0 || head_dim <= 0)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "total_tokens must be >= 0; num_heads and head_dim must be positive.");
+    if (head_dim % 16 != 0) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "dequantize_v: head_dim must be a multiple of 16.");
+    if (total_tokens > 0 && (!packed || !scale || !zero || !out))
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "dequantize_v: NULL pointer argument.");
+    return launch_dequantize_v(packed, scale, zero, out, total_tokens, num_heads, head_dim, meta_fp16,
+                               as_stream(stream));
+}
+
+int tt_fused_attention_decode(const float* Q, const float* dense_K, const float* dense_V, int dense_count,
+                              const int32_t* PBS_K_Packed, const void* PBS_K_Scales, const void* PBS_K_Zeroes,
+                              const int32_t* PBS_V_Packed, const void* PBS_V_Scales, const void* PBS_V_Zeroes,
+                              const int64_t* PBS_token_ids, int num_blocks, int num_q_heads, int num_kv_heads,
+                              int head_dim, float* attn_output, float* mean_attn_weights, int k_group_size,
+                              int meta_fp16, void* stream) {
+    clear_error();
+    return fused_impl(Q, dense_K, dense_V, dense_count, PBS_K_Packed, PBS_K_Scales, PBS_K_Zeroes, PBS_V_Packed,
+                      PBS_V_Scales, PBS_V_Zeroes, PBS_token_ids, num_blocks, num_q_heads, num_kv_heads, head_dim,
+                      attn_output, mean_attn_weights, k_group_size, meta_fp16, nullptr, 0, true, kBoth, 0,
+                      as_stream(stream));
+}
+
+size_t tt_fused_attention_workspace_bytes(int dense_count, int num_blocks, int num_q_heads, int num_kv_heads,
+                                          int head_dim, int k_group_size, int want_mean_weights) {
+    if (dense_count < 0 || num_blocks < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
+    return attn_plan(dense_count, num_blocks, num_q_heads, num_kv_heads, head_dim, k_group_size,
+                     want_mean_weights != 0)
+        .bytes;
+}
+
+int tt_fused_attention_decode_ws(const float* Q, const float* dense_K, const float* dense_V, int dense_count,
+                                 const int32_t* PBS_K_Packed, const void* PBS_K_Scales, const void* PBS_K_Zeroes,
+                                 const int32_t* PBS_V_Packed, const void* PBS_V_Scales, const void* PBS_V_Zeroes,
+                                 const int64_t* PBS_token_ids, int num_blocks, int num_q_heads, int num_kv_heads,
+                                 int head_dim, float* attn_output, float* mean_attn_weights, int k_group_size,
+                                 int meta_fp16, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    return fused_impl(Q, dense_K, dense_V, dense_count, PBS_K_Packed, PBS_K_Scales, PBS_K_Zeroes, PBS_V_Packed,
+                      PBS_V_Scales, PBS_V_Zeroes, PBS_token_ids, num_blocks, num_q_heads, num_kv_heads, head_dim,
+                      attn_output, mean_attn_weights, k_group_size, meta_fp16, workspace, workspace_bytes, false,
+                      kBoth, 0, as_stream(stream));
+}
+
+int tt_attention_partials(const float* Q, const float* dense_K, const float* dense_V, int dense_count,
+                          const int32_t* PBS_K_Packed, const void* PBS_K_Scales, const void* PBS_K_Zeroes,
+                          const int32_t* PBS_V_Packed, const void* PBS_V_Scales, const void* PBS_V_Zeroes,
+                          const int64_t* PBS_token_ids, int num_blocks, int num_q_heads, int num_kv_heads, int head_dim,
+                          int k_group_size, int meta_fp16, int want_mean_weights, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+    clear_error();
+    return fused_impl(Q, dense_K, dense_V, dense_count, PBS_K_Packed, PBS_K_Scales, PBS_K_Zeroes, PBS_V_Packed,
+                      PBS_V_Scales, PBS_V_Zeroes, PBS_token_ids, num_blocks, num_q_heads, num_kv_heads, head_dim,
+                      nullptr, nullptr, k_group_size, meta_fp16, workspace, workspace_bytes, false, kPartials,
+                      want_mean_weights, as_stream(stream));
+}
+
+int tt_attention_finalize(const float* Q, int dense_count, int num_blocks, int num_q_heads, int num_kv_heads,
+                          int head_dim, float* attn_output, float* mean_attn_weights, int k_group_size,
+                          int want_mean_weights, void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    // The finalize phase reads only the workspace; the tier pointers are not
+    // dereferenced, so placeholders satisfy the shared validation.
+    const void* ph = workspace;
+    return fused_impl(Q, static_cast<const float*>(ph), static_cast<const float*>(ph), dense_count,
+                      static_cast<const int32_t*>(ph), ph, ph, static_cast<const int32_t*>(ph), ph, ph,
+                      static_cast<const int64_t*>(ph), num_blocks, num_q_heads, num_kv_heads, head_dim, attn_output,
+                      mean_attn_weights, k_group_size, 0, workspace, workspace_bytes, false, kFinalize,
+                      want_mean_weights, as_stream(stream));
+}
+
+}  // extern "C"

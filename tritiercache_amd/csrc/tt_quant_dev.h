@@ -1,0 +1,93 @@
+// tt_quant_dev.h -- device functions for the bit-exact 2-bit quantisers.
+// Used by the standalone kernels (tt_quant.hip) and by the engine's
+// waiting-room flush (tt_engine.hip).
+#pragma once
+#include "tt_common.h"
+
+namespace tt {
+
+// K, one channel of one block (quantize_k_avx2.cpp:26-110). `src` points at
+// token 0 of the channel, tokens `tok_stride` floats apart. `vec` selects the
+// 8-wide vector body semantics (channel < 8*floor(D/8)) versus the scalar tail.
+// Writes scale/zero and kgs/16 words spaced `word_stride` apart.
+template <typename MetaT>
+__device__ __forceinline__ void quant_k_channel(const float* __restrict__ src, size_t tok_stride, int kgs, bool vec,
+                                                MetaT* scale_dst, MetaT* zero_dst, uint32_t* packed_dst,
+                                                size_t word_stride) {
+    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+    for (int t = 0; t < kgs; ++t) {
+        const float x = src[t * tok_stride];
+        if (vec) {
+            mn = x86_minps(mn, x);
+            mx = x86_maxps(mx, x);
+        } else {
+            mn = std_min(mn, x);
+            mx = std_max(mx, x);
+        }
+    }
+    const float d3 = (mx - mn) / 3.0f;
+    const float s = vec ? x86_maxps(d3, 1e-9f) : std_max(d3, 1e-9f);
+    Meta<MetaT>::store(scale_dst, 0, s);
+    Meta<MetaT>::store(zero_dst, 0, mn);
+    const int words = kgs / 16;
+    for (int w = 0; w < words; ++w) {
+        uint32_t bits = 0;
+        for (int st = 0; st < 16; ++st) {
+            const float x = src[(w * 16 + st) * tok_stride];
+            int q = cvt_rne_i32((x - mn) / s);
+            if (vec) {
+                q = q > 0 ? q : 0;
+                q = q < 3 ? q : 3;
+            } else {
+                q = q < 3 ? q : 3;
+                q = q > 0 ? q : 0;
+            }
+            bits |= static_cast<uint32_t>(q) << (2 * st);
+        }
+        packed_dst[w * word_stride] = bits;
+    }
+}
+
+// hmin8 / hmax8 reduction trees (quantize_v_avx2.cpp:7-23).
+__device__ __forceinline__ float hmin8(const float* x) {
+    const float m0 = x86_minps(x[0], x[4]), m1 = x86_minps(x[1], x[5]);
+    const float m2 = x86_minps(x[2], x[6]), m3 = x86_minps(x[3], x[7]);
+    return x86_minps(x86_minps(m0, m2), x86_minps(m1, m3));
+}
+__device__ __forceinline__ float hmax8(const float* x) {
+    const float m0 = x86_maxps(x[0], x[4]), m1 = x86_maxps(x[1], x[5]);
+    const float m2 = x86_maxps(x[2], x[6]), m3 = x86_maxps(x[3], x[7]);
+    return x86_maxps(x86_maxps(m0, m2), x86_maxps(m1, m3));
+}
+
+// V, one (token, head) row of D channels, D % 16 == 0
+// (quantize_v_avx2.cpp:44-108). Channel 16g+i lands in bits 2i of word g.
+template <typename MetaT>
+__device__ __forceinline__ void quant_v_row(const float* __restrict__ v, int D, MetaT* scale_dst, MetaT* zero_dst,
+                                            int32_t* packed_dst) {
+    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+    for (int c = 0; c < D; c += 8) {
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = v[c + j];
+        mn = std_min(mn, hmin8(x));
+        mx = std_max(mx, hmax8(x));
+    }
+    const float s = std_max((mx - mn) / 3.0f, 1e-9f);
+    Meta<MetaT>::store(scale_dst, 0, s);
+    Meta<MetaT>::store(zero_dst, 0, mn);
+    const int qhd = D / 16;
+    for (int g = 0; g < qhd; ++g) {
+        uint32_t bits = 0;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int q = cvt_rne_i32((v[g * 16 + i] - mn) / s);
+            q = q < 3 ? q : 3;
+            q = q > 0 ? q : 0;
+            bits |= static_cast<uint32_t>(q) << (2 * i);
+        }
+        packed_dst[g] = static_cast<int32_t>(bits);
+    }
+}
+
+}  // namespace tt
