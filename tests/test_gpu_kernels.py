@@ -142,7 +142,7 @@ def test_quantize_host_buffers_like_reference_tests(C, oracle):
     zero = np.zeros((1, 4, 64), np.uint16)
     C.quantize_k_block(K, packed[0], scale[0], zero[0], 4, 64, 16, "fp16")
     p, s, z = oracle.quantize_k(K, 16, True)
-    assert same_bits(packed[0], p) and same_bits(scale[0], s) and same_bits(zero[0], z)
+    assert same_bits(packed[0], p[0]) and same_bits(scale[0], s) and same_bits(zero[0], z)
     out = np.zeros((16, 4, 64), np.float32)
     C.dequantize_k(packed, scale, zero, out, 1, 4, 64, 16, "fp16")
     assert same_bits(out, oracle.dequantize_k(p, s, z, 1, 4, 64, 16, True))
