@@ -203,7 +203,7 @@ def main():
                         "partials")
                 b.record()
                 L.check(lib.tt_attention_finalize(d["Q"].data_ptr(), nd, nb, Hq, Hkv, D, d["out"].data_ptr(),
-                                                  d["mw"].data_ptr(), 16, 1, ws.data_ptr(), ws_bytes, sp()),
+                                                  d["mw"].data_ptr(), 16, f16, 1, ws.data_ptr(), ws_bytes, sp()),
                         "finalize")
                 evs.append((a, b))
         torch.cuda.synchronize()

@@ -139,8 +139,9 @@ TT_API int tt_attention_partials(const float* Q, const float* dense_K, const flo
                                  void* workspace, size_t workspace_bytes, void* stream);
 TT_API int tt_attention_finalize(const float* Q, int dense_count, int num_blocks, int num_q_heads,
                                  int num_kv_heads, int head_dim, float* attn_output,
-                                 float* mean_attn_weights, int k_group_size, int want_mean_weights,
-                                 void* workspace, size_t workspace_bytes, void* stream);
+                                 float* mean_attn_weights, int k_group_size, int meta_fp16,
+                                 int want_mean_weights, void* workspace, size_t workspace_bytes,
+                                 void* stream);
 
 /* ---------------------------------------------------------------------------
  * Engine: replaces _C.TriTierCacheEngine (bindings.cpp:384-626, class

@@ -41,7 +41,7 @@ _SIGNATURES = {
                                           _vp, _vp, _i, _i, _vp, _sz, _vp]),
     "tt_attention_partials": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
                                    _i, _vp, _sz, _vp]),
-    "tt_attention_finalize": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _vp, _sz, _vp]),
+    "tt_attention_finalize": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
     "tt_engine_create": (_i, [C.POINTER(_vp), _i, _i, _i, _i, _i, _i, _f, _f, _i, _i, C.c_char_p, _vp]),
     "tt_engine_destroy": (_i, [_vp]),
     "tt_engine_step": (_i, [_vp, _vp, _vp, _vp, _vp, _vp]),

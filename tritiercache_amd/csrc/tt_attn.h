@@ -65,7 +65,7 @@ struct AttnPlan {
 };
 
 // Plans the split-K launch for an upper bound of dense tokens / blocks.
-AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs, bool need_logits);
+AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs, bool need_logits, int meta_fp16);
 
 // Enqueues split + merge (+ mean weights / feedback / per-head weights).
 // mean_w: [token count] or null; head_w: [Hq, head_w_ld] or null.

@@ -26,6 +26,9 @@
 #include "tt_attn.h"
 
 #include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
 
 namespace tt {
 
@@ -369,26 +372,72 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
     }
 }
 
-// One workgroup per query head, one thread per channel.
+// LSE merge of the split partials of one query head. 256 threads: the
+// (max, sum) pairs are staged in LDS, the per-split weights exp(m_j - M) are
+// computed once, and the weighted accumulators are summed with the splits
+// divided between thread groups and the loads unrolled, so the kernel is
+// bound by one pass over the partials rather than by load latency.
 __global__ void __launch_bounds__(256) attn_merge_kernel(const float* __restrict__ part_ml,
                                                          const float* __restrict__ part_acc, int nsplit, int D,
                                                          float* __restrict__ out, float* __restrict__ rowstat) {
+    extern __shared__ float sh[];
+    float* fw = sh;                 // [nsplit] weights
+    float* red = sh + nsplit;       // [256] scratch
     const int h = blockIdx.x;
-    const int c = threadIdx.x;
+    const int tid = threadIdx.x;
     const float* ml = part_ml + static_cast<size_t>(h) * nsplit * 2;
-    float M = kNegInf;
-    for (int j = 0; j < nsplit; ++j) M = fmaxf(M, ml[2 * j]);
-    float L = 0.0f, A = 0.0f;
-    if (M != kNegInf) {
-        for (int j = 0; j < nsplit; ++j) {
-            const float mj = ml[2 * j];
-            const float f = (mj == kNegInf) ? 0.0f : exp2f((mj - M) * kLog2e);
-            L = __builtin_fmaf(f, ml[2 * j + 1], L);
-            if (c < D) A = __builtin_fmaf(f, part_acc[(static_cast<size_t>(h) * nsplit + j) * D + c], A);
-        }
+    float mx = kNegInf;
+    for (int j = tid; j < nsplit; j += 256) mx = fmaxf(mx, ml[2 * j]);
+    red[tid] = mx;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if (tid < st) red[tid] = fmaxf(red[tid], red[tid + st]);
+        __syncthreads();
     }
-    if (c < D) out[static_cast<size_t>(h) * D + c] = (L > 0.0f) ? A / L : 0.0f;
-    if (c == 0) {
+    const float M = red[0];
+    __syncthreads();
+    float lsum = 0.0f;
+    for (int j = tid; j < nsplit; j += 256) {
+        const float mj = ml[2 * j];
+        const float f = (M == kNegInf || mj == kNegInf) ? 0.0f : exp2f((mj - M) * kLog2e);
+        fw[j] = f;
+        lsum = __builtin_fmaf(f, ml[2 * j + 1], lsum);
+    }
+    red[tid] = lsum;
+    __syncthreads();
+    for (int st = 128; st > 0; st >>= 1) {
+        if (tid < st) red[tid] += red[tid + st];
+        __syncthreads();
+    }
+    const float L = red[0];
+    __syncthreads();
+    // Thread groups of D threads split the splits; each thread owns channel c.
+    const int groups = 256 / D;
+    const int grp = tid / D, c = tid - grp * D;
+    float A = 0.0f;
+    if (grp < groups) {
+        const float* base = part_acc + static_cast<size_t>(h) * nsplit * D + c;
+        int j = grp;
+        for (; j + 3 * groups < nsplit; j += 4 * groups) {
+            const float a0 = base[static_cast<size_t>(j) * D];
+            const float a1 = base[static_cast<size_t>(j + groups) * D];
+            const float a2 = base[static_cast<size_t>(j + 2 * groups) * D];
+            const float a3 = base[static_cast<size_t>(j + 3 * groups) * D];
+            A = __builtin_fmaf(fw[j], a0, A);
+            A = __builtin_fmaf(fw[j + groups], a1, A);
+            A = __builtin_fmaf(fw[j + 2 * groups], a2, A);
+            A = __builtin_fmaf(fw[j + 3 * groups], a3, A);
+        }
+        for (; j < nsplit; j += groups) A = __builtin_fmaf(fw[j], base[static_cast<size_t>(j) * D], A);
+    }
+    red[tid] = A;
+    __syncthreads();
+    if (tid < D) {
+        float o = 0.0f;
+        for (int g = 0; g < groups; ++g) o += red[g * D + tid];
+        out[static_cast<size_t>(h) * D + tid] = (L > 0.0f) ? o / L : 0.0f;
+    }
+    if (tid == 0) {
         rowstat[2 * h] = M;
         rowstat[2 * h + 1] = L;
     }
@@ -408,9 +457,19 @@ struct MeanArgs {
     Feedback fb;
 };
 
-// One thread per attended token: w_h = exp(s_h - max_h) / sum_h summed over
-// heads in order h = 0..Hq-1 and divided by Hq (fused_attn_avx2.cpp:286-300).
-__global__ void __launch_bounds__(256) attn_mean_kernel(MeanArgs a) {
+// One thread per attended token, one wave per workgroup so the grid covers
+// every CU: w_h = exp(s_h - max_h) / sum_h summed over h = 0..Hq-1 in order
+// and divided by Hq (fused_attn_avx2.cpp:286-300), then the engine's decayed
+// score feedback for that token (cache_engine.cpp:511-540).
+__global__ void __launch_bounds__(64) attn_mean_kernel(MeanArgs a) {
+    extern __shared__ float sh[];  // [Hq] max*log2e, [Hq] 1/sum
+    for (int h = threadIdx.x; h < a.Hq; h += blockDim.x) {
+        const float M = a.rowstat[2 * h];
+        const float L = a.rowstat[2 * h + 1];
+        sh[h] = M * kLog2e;
+        sh[a.Hq + h] = 1.0f / (L > 0.0f ? L : 1.0f);
+    }
+    __syncthreads();
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     int n = a.n_static;
     int s = 0, hh = 0, rw = 0, total = 0, Nd = 0;
@@ -423,16 +482,24 @@ __global__ void __launch_bounds__(256) attn_mean_kernel(MeanArgs a) {
         n = Nd + a.state[kBlocksUsed] * a.kgs;
     }
     if (i >= n) return;
+    const float* lg = a.logits + i;
     float sum = 0.0f;
-    for (int h = 0; h < a.Hq; ++h) {
-        const float sc = a.logits[static_cast<size_t>(h) * a.ld + i];
-        float w = 0.0f;
-        if (sc != kNegInf) {
-            const float M = a.rowstat[2 * h];
-            const float L = a.rowstat[2 * h + 1];
-            w = expf(sc - M) / (L > 0.0f ? L : 1.0f);
+    int h = 0;
+    for (; h + 8 <= a.Hq; h += 8) {
+        float sc[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) sc[u] = lg[static_cast<size_t>(h + u) * a.ld];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float w = (sc[u] == kNegInf) ? 0.0f : exp2f(__builtin_fmaf(sc[u], kLog2e, -sh[h + u])) * sh[a.Hq + h + u];
             sum += w;
+            if (a.head_w && i < a.head_w_ld) a.head_w[static_cast<size_t>(h + u) * a.head_w_ld + i] = w;
         }
+    }
+    for (; h < a.Hq; ++h) {
+        const float sc = lg[static_cast<size_t>(h) * a.ld];
+        const float w = (sc == kNegInf) ? 0.0f : exp2f(__builtin_fmaf(sc, kLog2e, -sh[h])) * sh[a.Hq + h];
+        sum += w;
         if (a.head_w && i < a.head_w_ld) a.head_w[static_cast<size_t>(h) * a.head_w_ld + i] = w;
     }
     const float mean = sum / static_cast<float>(a.Hq);
@@ -480,6 +547,54 @@ int launch_split_g(const SplitArgs& a, dim3 grid, int gp, int meta_fp16, hipStre
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
+int gp_for(int G) { return G >= 8 ? 8 : (G > 4 ? 8 : (G > 2 ? 4 : G)); }
+
+template <int CPL>
+const void* split_kernel_ptr(int gp, int fp16) {
+    switch (gp) {
+    case 1: return fp16 ? reinterpret_cast<const void*>(&attn_split_kernel<CPL, 1, uint16_t>)
+                        : reinterpret_cast<const void*>(&attn_split_kernel<CPL, 1, float>);
+    case 2: return fp16 ? reinterpret_cast<const void*>(&attn_split_kernel<CPL, 2, uint16_t>)
+                        : reinterpret_cast<const void*>(&attn_split_kernel<CPL, 2, float>);
+    case 4: return fp16 ? reinterpret_cast<const void*>(&attn_split_kernel<CPL, 4, uint16_t>)
+                        : reinterpret_cast<const void*>(&attn_split_kernel<CPL, 4, float>);
+    default: return fp16 ? reinterpret_cast<const void*>(&attn_split_kernel<CPL, 8, uint16_t>)
+                         : reinterpret_cast<const void*>(&attn_split_kernel<CPL, 8, float>);
+    }
+}
+
+// Resident split workgroups the device holds at once for this instantiation:
+// CUs x occupancy (queried once per device and shape, then cached).
+int resident_split_wgs(int D, int G, int fp16) {
+    static std::mutex mu;
+    static std::map<std::tuple<int, int, int, int>, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 1024;
+    const int gp = gp_for(G);
+    const auto key = std::make_tuple(dev, D, gp, fp16);
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    const void* fn = nullptr;
+    switch (D) {
+    case 16: fn = split_kernel_ptr<1>(gp, fp16); break;
+    case 32: fn = split_kernel_ptr<2>(gp, fp16); break;
+    case 64: fn = split_kernel_ptr<4>(gp, fp16); break;
+    case 128: fn = split_kernel_ptr<8>(gp, fp16); break;
+    default: fn = split_kernel_ptr<16>(gp, fp16); break;
+    }
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess || per_cu <= 0) {
+        (void)hipGetLastError();
+        per_cu = 2;
+    }
+    const int r = cus * per_cu;
+    cache[key] = r;
+    return r;
+}
+
 }  // namespace
 
 int attn_check_shapes(int Hq, int Hkv, int D, int kgs) {
@@ -492,15 +607,16 @@ int attn_check_shapes(int Hq, int Hkv, int D, int kgs) {
     return TT_OK;
 }
 
-AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs, bool need_logits) {
+AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs, bool need_logits, int meta_fp16) {
     AttnPlan p;
     const int W = kgs / 16;
     const long long units = static_cast<long long>((dense_ub + 15) / 16) * 8 + static_cast<long long>(blocks_ub) * W;
-    // About four workgroups per CU (256 CUs), but at least ~32 packed-tile
-    // units of work per workgroup so the per-split merge traffic stays small.
+    // One round of resident workgroups over all CUs, but at least ~32
+    // packed-tile units of work per workgroup so the merge traffic stays small.
     const int G = Hq / Hkv;
     const int chunks = (G + 7) / 8;
-    long long want = (1024 + static_cast<long long>(Hkv) * chunks - 1) / (static_cast<long long>(Hkv) * chunks);
+    const long long resident = resident_split_wgs(D, G, meta_fp16);
+    long long want = (resident + static_cast<long long>(Hkv) * chunks - 1) / (static_cast<long long>(Hkv) * chunks);
     long long cap = std::max<long long>(1, units / 32);
     p.nsplit = static_cast<int>(std::max<long long>(1, std::min(want, cap)));
     p.token_ub = dense_ub + blocks_ub * kgs;
@@ -532,7 +648,7 @@ int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipS
     a.wd = 8;
     a.wp = 1;
     const int G = in.Hq / in.Hkv;
-    const int gp = G >= 8 ? 8 : (G > 4 ? 8 : (G > 2 ? 4 : G));
+    const int gp = gp_for(G);
     const dim3 grid(plan.nsplit, in.Hkv, (G + gp - 1) / gp);
     switch (in.D) {
     case 16: return launch_split_g<1>(a, grid, gp, in.meta_fp16, stream);
@@ -549,8 +665,8 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
     const float* part_ml = reinterpret_cast<const float*>(base + plan.off_ml);
     const float* part_acc = reinterpret_cast<const float*>(base + plan.off_acc);
     float* rowstat = reinterpret_cast<float*>(base + plan.off_rowstat);
-    const int mthreads = std::max(64, (in.D + 63) / 64 * 64);
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(in.Hq), dim3(mthreads), 0, stream, part_ml, part_acc, plan.nsplit,
+    const size_t merge_lds = sizeof(float) * (static_cast<size_t>(plan.nsplit) + 256);
+    hipLaunchKernelGGL(attn_merge_kernel, dim3(in.Hq), dim3(256), merge_lds, stream, part_ml, part_acc, plan.nsplit,
                        in.D, out, rowstat);
     TT_LAUNCH_CHECK();
     if (plan.logits && (mean_w || head_w || (fb && fb->g))) {
@@ -567,7 +683,7 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
         m.head_w_ld = head_w_ld;
         m.fb = fb ? *fb : Feedback{};
         const int n = std::max(plan.token_ub, 1);
-        hipLaunchKernelGGL(attn_mean_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, m);
+        hipLaunchKernelGGL(attn_mean_kernel, dim3((n + 63) / 64), dim3(64), sizeof(float) * 2 * in.Hq, stream, m);
         TT_LAUNCH_CHECK();
     }
     return TT_OK;

@@ -64,7 +64,7 @@ int prepare(const float* Q, const float* dK, const float* dV, int dense_count, c
         TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'dense_K'/'dense_V' pointer address is NULL.");
     if (num_blocks > 0 && (!KP || !KS || !KZ || !VP || !VS || !VZ || !ids))
         TT_FAIL(TT_ERR_INVALID_ARGUMENT, "PBS arguments must be non-NULL when num_blocks > 0.");
-    *plan = attn_plan(dense_count, num_blocks, Hq, Hkv, D, kgs, want_mw);
+    *plan = attn_plan(dense_count, num_blocks, Hq, Hkv, D, kgs, want_mw, meta_fp16);
     in->Q = Q;
     in->k0 = dK;
     in->v0 = dV;
@@ -205,9 +205,13 @@ int tt_fused_attention_decode(const float* Q, const float* dense_K, const float*
 size_t tt_fused_attention_workspace_bytes(int dense_count, int num_blocks, int num_q_heads, int num_kv_heads,
                                           int head_dim, int k_group_size, int want_mean_weights) {
     if (dense_count < 0 || num_blocks < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
-    return attn_plan(dense_count, num_blocks, num_q_heads, num_kv_heads, head_dim, k_group_size,
-                     want_mean_weights != 0)
-        .bytes;
+    // The largest plan over both metadata types (their split counts can differ).
+    size_t b = 0;
+    for (int f = 0; f < 2; ++f)
+        b = std::max(b, attn_plan(dense_count, num_blocks, num_q_heads, num_kv_heads, head_dim, k_group_size,
+                                  want_mean_weights != 0, f)
+                            .bytes);
+    return b;
 }
 
 int tt_fused_attention_decode_ws(const float* Q, const float* dense_K, const float* dense_V, int dense_count,
@@ -237,7 +241,7 @@ int tt_attention_partials(const float* Q, const float* dense_K, const float* den
 }
 
 int tt_attention_finalize(const float* Q, int dense_count, int num_blocks, int num_q_heads, int num_kv_heads,
-                          int head_dim, float* attn_output, float* mean_attn_weights, int k_group_size,
+                          int head_dim, float* attn_output, float* mean_attn_weights, int k_group_size, int meta_fp16,
                           int want_mean_weights, void* workspace, size_t workspace_bytes, void* stream) {
     clear_error();
     // The finalize phase reads only the workspace; the tier pointers are not
@@ -246,7 +250,7 @@ int tt_attention_finalize(const float* Q, int dense_count, int num_blocks, int n
     return fused_impl(Q, static_cast<const float*>(ph), static_cast<const float*>(ph), dense_count,
                       static_cast<const int32_t*>(ph), ph, ph, static_cast<const int32_t*>(ph), ph, ph,
                       static_cast<const int64_t*>(ph), num_blocks, num_q_heads, num_kv_heads, head_dim, attn_output,
-                      mean_attn_weights, k_group_size, 0, workspace, workspace_bytes, false, kFinalize,
+                      mean_attn_weights, k_group_size, meta_fp16, workspace, workspace_bytes, false, kFinalize,
                       want_mean_weights, as_stream(stream));
 }
 

@@ -490,7 +490,7 @@ int engine_reserve_blocks(tt_engine* e, int need, hipStream_t s) {
     e->PBS_ids = ids;
     e->cap_blocks = nc;
     // Attention workspace follows the capacity.
-    const AttnPlan p = attn_plan(e->S + e->max_hh + e->R, nc, e->Hq, e->Hkv, e->D, e->kgs, true);
+    const AttnPlan p = attn_plan(e->S + e->max_hh + e->R, nc, e->Hq, e->Hkv, e->D, e->kgs, true, e->fp16);
     if (p.bytes > e->ws_bytes) {
         if (e->ws) {
             TT_HIP_CHECK(hipStreamSynchronize(s));
@@ -749,7 +749,7 @@ static int engine_attend(tt_engine* e, const float* Q, float* out, float* head_w
                          hipStream_t s) {
     int rc = engine_reserve_blocks(e, e->blocks_ub, s);
     if (rc) return rc;
-    const AttnPlan p = attn_plan(e->S + e->max_hh + e->R, e->blocks_ub, e->Hq, e->Hkv, e->D, e->kgs, true);
+    const AttnPlan p = attn_plan(e->S + e->max_hh + e->R, e->blocks_ub, e->Hq, e->Hkv, e->D, e->kgs, true, e->fp16);
     AttnInputs in = engine_inputs(e, Q);
     Feedback fb = engine_feedback_args(e);
     return attn_launch(in, p, e->ws, out, e->mw, feedback ? &fb : nullptr, head_w, head_w_ld, s);
