@@ -12,7 +12,8 @@ every step streams from HBM, not from the 256 MB Infinity Cache.
 
 One step = for each of the 32 layers, tt_fused_attention_decode_ws (split-K
 partials, log-sum-exp merge, mean attention weights), replayed as one HIP graph.
-The dominant kernel (attn_split_kernel) is also timed on its own with HIP
+The dominant kernel (attn_tiles_kernel: split-K partials over the FP32 tiles
+and, on the matrix cores, the packed blocks) is also timed on its own with HIP
 events on the launch stream, for the roofline.
 
 The CPU baseline is the reference's own AVX2+OpenMP kernel
@@ -193,7 +194,7 @@ def main():
         return e0.elapsed_time(e1) * 1000.0 / args.steps, g is not None
 
     def time_split_kernel(t, f16, reps):
-        """Average duration of one attn_split_kernel launch (HIP events on the launch stream)."""
+        """Average duration of one attn_tiles_kernel launch (HIP events on the launch stream)."""
         evs = []
         for _ in range(reps):
             for d in data:
@@ -289,7 +290,7 @@ def main():
         "bytes_read_per_step": bpl * layers,
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_split_kernel",
+            "kernel": "attn_tiles_kernel",
             "achieved": round(kern_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

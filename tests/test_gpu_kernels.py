@@ -218,6 +218,12 @@ SWEEP = [
     (4, 2, 256, 18, 4, 16, True, "holes"),
     (8, 8, 256, 3, 3, 32, False, "none"),
     (3, 3, 64, 64, 8, 16, False, "all"),
+    # head_dim 128 runs the matrix-core path over the packed store
+    (32, 8, 128, 50, 9, 32, False, "holes"),
+    (16, 2, 128, 20, 5, 32, True, "tail"),
+    (16, 1, 128, 10, 6, 16, False, "none"),
+    (8, 8, 128, 0, 1, 16, False, "none"),
+    (7, 1, 128, 0, 3, 16, True, "block"),
 ]
 
 
@@ -235,6 +241,34 @@ def test_fused_attention_vs_oracle(C, oracle, case):
     ids = args[10]
     if nb:
         assert np.all(mw[nd:][ids[: nb * kgs] == -1] == 0)
+
+
+@pytest.mark.parametrize("qs,ks,vs,voff", [(16.0, 50.0, 1000.0, 3000.0), (0.05, 0.01, 1e-3, 0.0), (1.0, 1.0, 1e-7, 1.0)])
+def test_fused_attention_extreme_scales(C, oracle, qs, ks, vs, voff):
+    """Q, K, V far from unit scale: the f16 operands of the matrix-core path are
+    normalised per head (Q) and per tile (p * v_scale)."""
+    Hq, Hkv, D, nd, nb, kgs = 16, 4, 128, 40, 24, 16
+    args = list(make_case(oracle, Hq, Hkv, D, nd, nb, kgs, False, "tail", seed=77))
+    rng = np.random.default_rng(77)
+    Kp = rng.standard_normal((nb * kgs, Hkv, D)).astype(np.float32) * np.float32(ks)
+    Vp = (rng.standard_normal((nb * kgs, Hkv, D)).astype(np.float32) * np.float32(vs) + np.float32(voff))
+    packs = [(oracle.quantize_k(Kp[b * kgs:(b + 1) * kgs], kgs, False),
+              oracle.quantize_v(Vp[b * kgs:(b + 1) * kgs], False)) for b in range(nb)]
+    args[0] = (args[0] * np.float32(qs)).astype(np.float32)
+    args[1] = (args[1] * np.float32(ks)).astype(np.float32)
+    args[2] = (args[2] * np.float32(vs) + np.float32(voff)).astype(np.float32)
+    args[4] = np.stack([k[0] for k, _ in packs])
+    args[5] = np.stack([k[1] for k, _ in packs])
+    args[6] = np.stack([k[2] for k, _ in packs])
+    args[7] = np.concatenate([v[0] for _, v in packs])
+    args[8] = np.concatenate([v[1] for _, v in packs])
+    args[9] = np.concatenate([v[2] for _, v in packs])
+    args = tuple(args)
+    out, mw = _run_fused_gpu(C, args)
+    ro, rmw = oracle.fused_attention_decode(*args)
+    assert np.all(np.isfinite(out)) and np.all(np.isfinite(mw))
+    assert rel_err(out, ro) <= ATTN_TOL, (qs, ks, vs, voff)
+    assert rel_err(mw, rmw) <= ATTN_TOL, (qs, ks, vs, voff)
 
 
 def test_fused_attention_without_mean_weights(C, oracle):

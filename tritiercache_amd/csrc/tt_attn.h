@@ -57,7 +57,9 @@ struct Feedback {
 };
 
 struct AttnPlan {
-    int nsplit = 1;
+    int nsplit = 1;      // partial slots per query head = nsplit_p + nsplit_d
+    int nsplit_p = 0;    // matrix-core workgroups over the packed store (head_dim 128)
+    int nsplit_d = 1;    // VALU workgroups
     int ld = 0;          // logits row stride (floats)
     int token_ub = 0;    // upper bound on attended tokens
     size_t off_ml = 0, off_acc = 0, off_rowstat = 0, off_logits = 0, bytes = 0;

@@ -112,22 +112,30 @@ __device__ __forceinline__ void load_meta(const MetaT* __restrict__ p, float (&x
 
 struct SplitArgs {
     AttnInputs in;
-    float inv_sqrt_d;
+    float scale2;  // log2(e) / sqrt(head_dim): logits are kept in log2 units
     float* part_ml;
     float* part_acc;
     float* logits;
     int ld;
-    int nsplit;
-    int wd, wp;  // tile cost weights: dense, packed
+    int nsplit;      // partial slots per query head
+    int nsplit_p;    // matrix-core workgroups over the packed store: slots [0, nsplit_p)
+    int nsplit_d;    // VALU workgroups: slots [nsplit_p, nsplit)
+    int dense_only;  // VALU workgroups take the FP32 tiles only
+    int wd, wp;      // tile cost weights: dense, packed
+};
+
+// LDS of the VALU tile loop: per-wave (max, sum, acc[D]) for the final merge.
+template <int D, int GP>
+struct SplitLds {
+    static constexpr int BYTES = 4 * GP * (2 + D) * 4;
 };
 
 // CPL: channels per lane (head_dim / 16). GP: query heads per workgroup
 // (padded to a power of two; heads past the group are zero and never stored).
 template <int CPL, int GP, typename MetaT>
-__global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
+__device__ __forceinline__ void split_body(const SplitArgs& a, const int split, char* lds) {
     constexpr int D = 16 * CPL;
     const AttnInputs& in = a.in;
-    const int split = blockIdx.x;
     const int kvh = blockIdx.y;
     const int G = in.Hq / in.Hkv;
     const int g0 = blockIdx.z * GP;
@@ -148,12 +156,12 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
     const int Nd = n0 + n1 + n2;
     const int W = in.kgs >> 4;
     const int Td = (Nd + 15) >> 4;
-    const int Tp = nb * W;
+    const int Tp = a.dense_only ? 0 : nb * W;
     const int Hkv = in.Hkv;
 
     // Cost-balanced contiguous tile range of this split.
     const long long U = static_cast<long long>(Td) * a.wd + static_cast<long long>(Tp) * a.wp;
-    const long long lo = U * split / a.nsplit, hi = U * (split + 1) / a.nsplit;
+    const long long lo = U * split / a.nsplit_d, hi = U * (split + 1) / a.nsplit_d;
     auto cdiv = [](long long x, long long y) -> long long { return x <= 0 ? 0 : (x + y - 1) / y; };
     const int d_begin = static_cast<int>(min(cdiv(lo, a.wd), static_cast<long long>(Td)));
     const int d_end = static_cast<int>(min(cdiv(hi, a.wd), static_cast<long long>(Td)));
@@ -280,7 +288,7 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int g = 0; g < GP; ++g) {
-                const float d = row_sum16(s[i][g]) * a.inv_sqrt_d;
+                const float d = row_sum16(s[i][g]) * a.scale2;
                 s[i][g] = valid[i] ? d : kNegInf;
             }
 
@@ -303,10 +311,10 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
             tm = fmaxf(tm, shfl_xor(tm, 16));
             tm = fmaxf(tm, shfl_xor(tm, 32));
             const float mn = fmaxf(m[g], tm);
-            const float alpha = (m[g] == kNegInf) ? 0.0f : exp2f((m[g] - mn) * kLog2e);
+            const float alpha = (m[g] == kNegInf) ? 0.0f : exp2f(m[g] - mn);
             float p[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] = (s[i][g] == kNegInf) ? 0.0f : exp2f((s[i][g] - mn) * kLog2e);
+            for (int i = 0; i < 4; ++i) p[i] = (s[i][g] == kNegInf) ? 0.0f : exp2f(s[i][g] - mn);
             l[g] = __builtin_fmaf(l[g], alpha, (p[0] + p[1]) + (p[2] + p[3]));
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
@@ -334,16 +342,17 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
     }
 
     // Merge the four waves in LDS and store one partial per query head.
-    __shared__ float sm_m[4][GP], sm_l[4][GP];
-    __shared__ float sm_acc[4][GP][D];
+    float* sm_m = reinterpret_cast<float*>(lds);  // [4][GP]
+    float* sm_l = sm_m + 4 * GP;                   // [4][GP]
+    float* sm_acc = sm_l + 4 * GP;                 // [4][GP][D]
     if (tg == 0) {
 #pragma unroll
         for (int g = 0; g < GP; ++g) {
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) sm_acc[wave][g][cp * CPL + j] = acc[g][j];
+            for (int j = 0; j < CPL; ++j) sm_acc[(wave * GP + g) * D + cp * CPL + j] = acc[g][j];
             if (cp == 0) {
-                sm_m[wave][g] = m[g];
-                sm_l[wave][g] = l[g];
+                sm_m[wave * GP + g] = m[g];
+                sm_l[wave * GP + g] = l[g];
             }
         }
     }
@@ -352,24 +361,47 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
         const int g = idx / D, c = idx - g * D;
         float M = kNegInf;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w][g]);
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w * GP + g]);
         float A = 0.0f, L = 0.0f;
         if (M != kNegInf) {
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
-                const float mw = sm_m[w][g];
-                const float f = (mw == kNegInf) ? 0.0f : exp2f((mw - M) * kLog2e);
-                A = __builtin_fmaf(f, sm_acc[w][g][c], A);
-                L = __builtin_fmaf(f, sm_l[w][g], L);
+                const float mw = sm_m[w * GP + g];
+                const float f = (mw == kNegInf) ? 0.0f : exp2f(mw - M);
+                A = __builtin_fmaf(f, sm_acc[(w * GP + g) * D + c], A);
+                L = __builtin_fmaf(f, sm_l[w * GP + g], L);
             }
         }
-        const size_t pi = static_cast<size_t>(kvh * G + g0 + g) * a.nsplit + split;
+        const size_t pi = static_cast<size_t>(kvh * G + g0 + g) * a.nsplit + a.nsplit_p + split;
         a.part_acc[pi * D + c] = A;
         if (c == 0) {
             a.part_ml[2 * pi] = M;
             a.part_ml[2 * pi + 1] = L;
         }
     }
+}
+
+template <int CPL, int GP, typename MetaT>
+__global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
+    __shared__ __align__(16) char lds[SplitLds<16 * CPL, GP>::BYTES];
+    split_body<CPL, GP, MetaT>(a, static_cast<int>(blockIdx.x), lds);
+}
+
+#include "tt_attn_mfma.h"
+
+// head_dim 128: workgroups [0, nsplit_p) run the matrix-core loop over the
+// packed store, the rest the VALU loop over the FP32 tiles, in one launch so
+// both kinds share the machine.
+template <int GP, typename MetaT>
+__global__ void __launch_bounds__(256) attn_tiles_kernel(SplitArgs a) {
+    constexpr int kMf = 4 * MfLds<GP>::BYTES;
+    constexpr int kVa = SplitLds<kMfD, GP>::BYTES;
+    __shared__ __align__(16) char lds[kMf > kVa ? kMf : kVa];
+    const int x = static_cast<int>(blockIdx.x);
+    if (x < a.nsplit_p)
+        packed_body<GP, MetaT>(a, x, lds);
+    else
+        split_body<8, GP, MetaT>(a, x - a.nsplit_p, lds);
 }
 
 // LSE merge of the split partials of one query head. 256 threads: the
@@ -399,7 +431,7 @@ __global__ void __launch_bounds__(256) attn_merge_kernel(const float* __restrict
     float lsum = 0.0f;
     for (int j = tid; j < nsplit; j += 256) {
         const float mj = ml[2 * j];
-        const float f = (M == kNegInf || mj == kNegInf) ? 0.0f : exp2f((mj - M) * kLog2e);
+        const float f = (M == kNegInf || mj == kNegInf) ? 0.0f : exp2f(mj - M);
         fw[j] = f;
         lsum = __builtin_fmaf(f, ml[2 * j + 1], lsum);
     }
@@ -462,11 +494,11 @@ struct MeanArgs {
 // and divided by Hq (fused_attn_avx2.cpp:286-300), then the engine's decayed
 // score feedback for that token (cache_engine.cpp:511-540).
 __global__ void __launch_bounds__(64) attn_mean_kernel(MeanArgs a) {
-    extern __shared__ float sh[];  // [Hq] max*log2e, [Hq] 1/sum
+    extern __shared__ float sh[];  // [Hq] row max (log2 units), [Hq] 1/sum
     for (int h = threadIdx.x; h < a.Hq; h += blockDim.x) {
         const float M = a.rowstat[2 * h];
         const float L = a.rowstat[2 * h + 1];
-        sh[h] = M * kLog2e;
+        sh[h] = M;
         sh[a.Hq + h] = 1.0f / (L > 0.0f ? L : 1.0f);
     }
     __syncthreads();
@@ -491,14 +523,14 @@ __global__ void __launch_bounds__(64) attn_mean_kernel(MeanArgs a) {
         for (int u = 0; u < 8; ++u) sc[u] = lg[static_cast<size_t>(h + u) * a.ld];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const float w = (sc[u] == kNegInf) ? 0.0f : exp2f(__builtin_fmaf(sc[u], kLog2e, -sh[h + u])) * sh[a.Hq + h + u];
+            const float w = (sc[u] == kNegInf) ? 0.0f : exp2f(sc[u] - sh[h + u]) * sh[a.Hq + h + u];
             sum += w;
             if (a.head_w && i < a.head_w_ld) a.head_w[static_cast<size_t>(h + u) * a.head_w_ld + i] = w;
         }
     }
     for (; h < a.Hq; ++h) {
         const float sc = lg[static_cast<size_t>(h) * a.ld];
-        const float w = (sc == kNegInf) ? 0.0f : exp2f(__builtin_fmaf(sc, kLog2e, -sh[h])) * sh[a.Hq + h];
+        const float w = (sc == kNegInf) ? 0.0f : exp2f(sc - sh[h]) * sh[a.Hq + h];
         sum += w;
         if (a.head_w && i < a.head_w_ld) a.head_w[static_cast<size_t>(h) * a.head_w_ld + i] = w;
     }
@@ -545,9 +577,41 @@ int launch_split_g(const SplitArgs& a, dim3 grid, int gp, int meta_fp16, hipStre
     }
 }
 
+template <int GP>
+int launch_tiles_meta(const SplitArgs& a, dim3 grid, int meta_fp16, hipStream_t st) {
+    if (meta_fp16)
+        hipLaunchKernelGGL((attn_tiles_kernel<GP, uint16_t>), grid, dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((attn_tiles_kernel<GP, float>), grid, dim3(256), 0, st, a);
+    TT_LAUNCH_CHECK();
+    return TT_OK;
+}
+
+int launch_tiles(const SplitArgs& a, dim3 grid, int gp, int meta_fp16, hipStream_t st) {
+    switch (gp) {
+    case 1: return launch_tiles_meta<1>(a, grid, meta_fp16, st);
+    case 2: return launch_tiles_meta<2>(a, grid, meta_fp16, st);
+    case 4: return launch_tiles_meta<4>(a, grid, meta_fp16, st);
+    default: return launch_tiles_meta<8>(a, grid, meta_fp16, st);
+    }
+}
+
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 int gp_for(int G) { return G >= 8 ? 8 : (G > 4 ? 8 : (G > 2 ? 4 : G)); }
+
+// The matrix-core path serves head_dim 128 with either block size.
+bool use_tiles_kernel(int D) { return D == kMfD; }
+
+template <typename MetaT>
+const void* tiles_kernel_ptr(int gp) {
+    switch (gp) {
+    case 1: return reinterpret_cast<const void*>(&attn_tiles_kernel<1, MetaT>);
+    case 2: return reinterpret_cast<const void*>(&attn_tiles_kernel<2, MetaT>);
+    case 4: return reinterpret_cast<const void*>(&attn_tiles_kernel<4, MetaT>);
+    default: return reinterpret_cast<const void*>(&attn_tiles_kernel<8, MetaT>);
+    }
+}
 
 template <int CPL>
 const void* split_kernel_ptr(int gp, int fp16) {
@@ -563,8 +627,8 @@ const void* split_kernel_ptr(int gp, int fp16) {
     }
 }
 
-// Resident split workgroups the device holds at once for this instantiation:
-// CUs x occupancy (queried once per device and shape, then cached).
+// Workgroups of the split launch the device holds at once: CUs x occupancy
+// (queried once per device and shape, then cached).
 int resident_split_wgs(int D, int G, int fp16) {
     static std::mutex mu;
     static std::map<std::tuple<int, int, int, int>, int> cache;
@@ -578,12 +642,15 @@ int resident_split_wgs(int D, int G, int fp16) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     const void* fn = nullptr;
-    switch (D) {
-    case 16: fn = split_kernel_ptr<1>(gp, fp16); break;
-    case 32: fn = split_kernel_ptr<2>(gp, fp16); break;
-    case 64: fn = split_kernel_ptr<4>(gp, fp16); break;
-    case 128: fn = split_kernel_ptr<8>(gp, fp16); break;
-    default: fn = split_kernel_ptr<16>(gp, fp16); break;
+    if (use_tiles_kernel(D)) {
+        fn = fp16 ? tiles_kernel_ptr<uint16_t>(gp) : tiles_kernel_ptr<float>(gp);
+    } else {
+        switch (D) {
+        case 16: fn = split_kernel_ptr<1>(gp, fp16); break;
+        case 32: fn = split_kernel_ptr<2>(gp, fp16); break;
+        case 64: fn = split_kernel_ptr<4>(gp, fp16); break;
+        default: fn = split_kernel_ptr<16>(gp, fp16); break;
+        }
     }
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 256, 0) != hipSuccess || per_cu <= 0) {
@@ -610,15 +677,29 @@ int attn_check_shapes(int Hq, int Hkv, int D, int kgs) {
 AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs, bool need_logits, int meta_fp16) {
     AttnPlan p;
     const int W = kgs / 16;
-    const long long units = static_cast<long long>((dense_ub + 15) / 16) * 8 + static_cast<long long>(blocks_ub) * W;
-    // One round of resident workgroups over all CUs, but at least ~32
-    // packed-tile units of work per workgroup so the merge traffic stays small.
     const int G = Hq / Hkv;
-    const int chunks = (G + 7) / 8;
+    const int chunks = (G + gp_for(G) - 1) / gp_for(G);
+    const long long heads = static_cast<long long>(Hkv) * chunks;
     const long long resident = resident_split_wgs(D, G, meta_fp16);
-    long long want = (resident + static_cast<long long>(Hkv) * chunks - 1) / (static_cast<long long>(Hkv) * chunks);
-    long long cap = std::max<long long>(1, units / 32);
-    p.nsplit = static_cast<int>(std::max<long long>(1, std::min(want, cap)));
+    const long long per_head = std::max<long long>(1, (resident + heads - 1) / heads);
+    const long long dense_tiles = (dense_ub + 15) / 16;
+    if (use_tiles_kernel(D)) {
+        // Dense workgroups take ~8 FP32 tiles (two per wave); the packed
+        // workgroups fill the rest of one resident round, with at least ~8
+        // pairs of tiles each so the partials stay small.
+        const long long pairs = (static_cast<long long>(blocks_ub) * W + 1) / 2;
+        p.nsplit_d = static_cast<int>(std::max<long long>(1, (dense_tiles + 7) / 8));
+        const long long want = std::max<long long>(1, per_head - p.nsplit_d);
+        p.nsplit_p = static_cast<int>(std::max<long long>(1, std::min(want, pairs / 8)));
+    } else {
+        // One round of resident workgroups, but at least ~32 packed-tile
+        // units of work per workgroup so the merge traffic stays small.
+        const long long units = dense_tiles * 8 + static_cast<long long>(blocks_ub) * W;
+        const long long cap = std::max<long long>(1, units / 32);
+        p.nsplit_p = 0;
+        p.nsplit_d = static_cast<int>(std::max<long long>(1, std::min(per_head, cap)));
+    }
+    p.nsplit = p.nsplit_p + p.nsplit_d;
     p.token_ub = dense_ub + blocks_ub * kgs;
     p.ld = (p.token_ub + 3) & ~3;
     p.logits = need_logits;
@@ -639,17 +720,25 @@ int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipS
     char* base = static_cast<char*>(ws);
     SplitArgs a;
     a.in = in;
-    a.inv_sqrt_d = 1.0f / sqrtf(static_cast<float>(in.D));
+    a.scale2 = kLog2e / sqrtf(static_cast<float>(in.D));
     a.part_ml = reinterpret_cast<float*>(base + plan.off_ml);
     a.part_acc = reinterpret_cast<float*>(base + plan.off_acc);
     a.logits = plan.logits ? reinterpret_cast<float*>(base + plan.off_logits) : nullptr;
     a.ld = plan.ld;
     a.nsplit = plan.nsplit;
+    a.nsplit_p = plan.nsplit_p;
+    a.nsplit_d = plan.nsplit_d;
+    a.dense_only = plan.nsplit_p > 0 ? 1 : 0;
     a.wd = 8;
     a.wp = 1;
     const int G = in.Hq / in.Hkv;
     const int gp = gp_for(G);
     const dim3 grid(plan.nsplit, in.Hkv, (G + gp - 1) / gp);
+    if (use_tiles_kernel(in.D)) {
+        if (plan.nsplit_p <= 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
+        return launch_tiles(a, grid, gp, in.meta_fp16, stream);
+    }
+    if (plan.nsplit_p != 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
     switch (in.D) {
     case 16: return launch_split_g<1>(a, grid, gp, in.meta_fp16, stream);
     case 32: return launch_split_g<2>(a, grid, gp, in.meta_fp16, stream);
