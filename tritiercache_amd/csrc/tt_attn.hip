@@ -3,26 +3,28 @@
 // Replaces the reference's fused_attention_decode_impl
 // (csrc/cpu/fused_attn_avx2.cpp:145-301), which dequantises every packed block
 // into a scratch buffer, stores a [Hq, N] score matrix and makes three passes.
-// Here each token's K/V bytes are read from HBM once:
+// Here each token's K/V bytes are read from HBM once. Logits are kept in
+// log2 units (dot * log2(e) / sqrt(D)) so every exponential is one v_exp_f32.
 //
-//   attn_split_kernel   grid (splits, Hkv, head-chunks), 256 threads = 4 waves.
+//   attn_packed_kernel  head_dim 128: the 2-bit packed blocks on the matrix
+//                       cores (tt_attn_mfma.h), grid (splits, Hkv, head
+//                       chunks), 4 waves; one (max, sum, acc[D]) partial per
+//                       (query head, split).
+//   attn_split_kernel   VALU loop, grid (splits, Hkv, head chunks), 4 waves.
 //                       A workgroup owns one KV head and a contiguous, cost-
-//                       balanced range of 16-token tiles (FP32 dense tiles
-//                       first, then 2-bit packed tiles). Each wave streams its
-//                       tiles with coalesced vector loads, unpacks the 2-bit
-//                       words in registers (fmaf(q, scale, zero), the
-//                       reference's dequant rounding), and folds them into the
-//                       QK dot products and the PV accumulation of all GQA query
-//                       heads of that KV head with an online softmax. Lanes are
-//                       (token group tg = lane/16) x (channel slice cp = lane%16);
-//                       QK partial sums reduce across the 16 channel lanes of a
-//                       row with DPP butterflies. Waves merge in LDS; one
-//                       (max, sum, acc[D]) partial per (query head, split).
-//   attn_merge_kernel   LSE merge of the partials -> attn_output, row max/sum.
-//   attn_mean_kernel    mean attention weights over query heads (:286-300),
-//                       optional per-head weights, and the engine's decayed
-//                       score feedback (cache_engine.cpp:511-540) in the same
-//                       pass.
+//                       balanced range of 16-token tiles: the FP32 tiers (with
+//                       head_dim 128 only these) and, for other head sizes,
+//                       the 2-bit tiles too, unpacked in registers with the
+//                       reference's dequant rounding fmaf(q, scale, zero).
+//                       Lanes are (token group tg = lane/16) x (channel slice
+//                       cp = lane%16); QK partial sums reduce across the 16
+//                       channel lanes of a row with DPP butterflies; online
+//                       softmax over all GQA query heads of the KV head.
+//   attn_finalize_kernel  LSE merge of the partials -> attn_output, and in the
+//                       same launch the mean attention weights over query
+//                       heads (:286-300), optional per-head weights and the
+//                       engine's decayed score feedback (cache_engine.cpp:
+//                       511-540).
 #include "tt_attn.h"
 
 #include <algorithm>
@@ -120,7 +122,6 @@ struct SplitArgs {
     int nsplit;      // partial slots per query head
     int nsplit_p;    // matrix-core workgroups over the packed store: slots [0, nsplit_p)
     int nsplit_d;    // VALU workgroups: slots [nsplit_p, nsplit)
-    int dense_only;  // VALU workgroups take the FP32 tiles only
     int wd, wp;      // tile cost weights: dense, packed
 };
 
@@ -156,7 +157,7 @@ __device__ __forceinline__ void split_body(const SplitArgs& a, const int split, 
     const int Nd = n0 + n1 + n2;
     const int W = in.kgs >> 4;
     const int Td = (Nd + 15) >> 4;
-    const int Tp = a.dense_only ? 0 : nb * W;
+    const int Tp = nb * W;
     const int Hkv = in.Hkv;
 
     // Cost-balanced contiguous tile range of this split.
@@ -389,98 +390,48 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
 
 #include "tt_attn_mfma.h"
 
-// head_dim 128: workgroups [0, nsplit_p) run the matrix-core loop over the
-// packed store, the rest the VALU loop over the FP32 tiles, in one launch so
-// both kinds share the machine.
+// head_dim 128: the matrix-core loop over the packed store, each workgroup
+// with a share of the FP32 tiles as a VALU prologue (grid nsplit_p x Hkv x
+// head chunks).
 template <int GP, typename MetaT>
-__global__ void __launch_bounds__(256) attn_tiles_kernel(SplitArgs a) {
-    constexpr int kMf = 4 * MfLds<GP>::BYTES;
-    constexpr int kVa = SplitLds<kMfD, GP>::BYTES;
-    __shared__ __align__(16) char lds[kMf > kVa ? kMf : kVa];
-    const int x = static_cast<int>(blockIdx.x);
-    if (x < a.nsplit_p)
-        packed_body<GP, MetaT>(a, x, lds);
-    else
-        split_body<8, GP, MetaT>(a, x - a.nsplit_p, lds);
+__global__ void __launch_bounds__(256) attn_packed_kernel(SplitArgs a) {
+    __shared__ __align__(16) char lds[MfLds<GP>::TOTAL];
+    // The KV heads of one tile sit side by side in memory (512-byte K rows,
+    // 32-byte V rows): rotate each head's split index so the workgroups that
+    // run together stream different regions instead of the same DRAM pages.
+    const int heads = static_cast<int>(gridDim.y * gridDim.z);
+    const int hid = static_cast<int>(blockIdx.y * gridDim.z + blockIdx.z);
+    const int rot = static_cast<int>(static_cast<unsigned>(a.nsplit_p) * static_cast<unsigned>(hid) /
+                                     static_cast<unsigned>(heads));
+    int split = static_cast<int>(blockIdx.x) + rot;
+    split = split >= a.nsplit_p ? split - a.nsplit_p : split;
+    packed_body<GP, MetaT>(a, __builtin_amdgcn_readfirstlane(split), lds);
 }
 
-// LSE merge of the split partials of one query head. 256 threads: the
-// (max, sum) pairs are staged in LDS, the per-split weights exp(m_j - M) are
-// computed once, and the weighted accumulators are summed with the splits
-// divided between thread groups and the loads unrolled, so the kernel is
-// bound by one pass over the partials rather than by load latency.
-__global__ void __launch_bounds__(256) attn_merge_kernel(const float* __restrict__ part_ml,
-                                                         const float* __restrict__ part_acc, int nsplit, int D,
-                                                         float* __restrict__ out, float* __restrict__ rowstat) {
-    extern __shared__ float sh[];
-    float* fw = sh;                 // [nsplit] weights
-    float* red = sh + nsplit;       // [256] scratch
-    const int h = blockIdx.x;
-    const int tid = threadIdx.x;
-    const float* ml = part_ml + static_cast<size_t>(h) * nsplit * 2;
-    float mx = kNegInf;
-    for (int j = tid; j < nsplit; j += 256) mx = fmaxf(mx, ml[2 * j]);
-    red[tid] = mx;
-    __syncthreads();
-    for (int st = 128; st > 0; st >>= 1) {
-        if (tid < st) red[tid] = fmaxf(red[tid], red[tid + st]);
-        __syncthreads();
-    }
-    const float M = red[0];
-    __syncthreads();
-    float lsum = 0.0f;
-    for (int j = tid; j < nsplit; j += 256) {
-        const float mj = ml[2 * j];
-        const float f = (M == kNegInf || mj == kNegInf) ? 0.0f : exp2f(mj - M);
-        fw[j] = f;
-        lsum = __builtin_fmaf(f, ml[2 * j + 1], lsum);
-    }
-    red[tid] = lsum;
-    __syncthreads();
-    for (int st = 128; st > 0; st >>= 1) {
-        if (tid < st) red[tid] += red[tid + st];
-        __syncthreads();
-    }
-    const float L = red[0];
-    __syncthreads();
-    // Thread groups of D threads split the splits; each thread owns channel c.
-    const int groups = 256 / D;
-    const int grp = tid / D, c = tid - grp * D;
-    float A = 0.0f;
-    if (grp < groups) {
-        const float* base = part_acc + static_cast<size_t>(h) * nsplit * D + c;
-        int j = grp;
-        for (; j + 3 * groups < nsplit; j += 4 * groups) {
-            const float a0 = base[static_cast<size_t>(j) * D];
-            const float a1 = base[static_cast<size_t>(j + groups) * D];
-            const float a2 = base[static_cast<size_t>(j + 2 * groups) * D];
-            const float a3 = base[static_cast<size_t>(j + 3 * groups) * D];
-            A = __builtin_fmaf(fw[j], a0, A);
-            A = __builtin_fmaf(fw[j + groups], a1, A);
-            A = __builtin_fmaf(fw[j + 2 * groups], a2, A);
-            A = __builtin_fmaf(fw[j + 3 * groups], a3, A);
-        }
-        for (; j < nsplit; j += groups) A = __builtin_fmaf(fw[j], base[static_cast<size_t>(j) * D], A);
-    }
-    red[tid] = A;
-    __syncthreads();
-    if (tid < D) {
-        float o = 0.0f;
-        for (int g = 0; g < groups; ++g) o += red[g * D + tid];
-        out[static_cast<size_t>(h) * D + tid] = (L > 0.0f) ? o / L : 0.0f;
-    }
-    if (tid == 0) {
-        rowstat[2 * h] = M;
-        rowstat[2 * h + 1] = L;
-    }
-}
-
-struct MeanArgs {
-    const float* logits;
-    int ld;
-    const float* rowstat;
+// ---------------------------------------------------------------------------
+// Finalize: one launch with two kinds of workgroups.
+//   [0, Hq)        merge the split partials of query head h (log2 units):
+//                  M = max_j m_j, L = sum_j l_j 2^(m_j - M),
+//                  out = sum_j acc_j 2^(m_j - M) / L.
+//   [Hq, ...)      mean attention weights of 256 tokens each
+//                  (fused_attn_avx2.cpp:286-300): every such workgroup first
+//                  rebuilds (M, 1/L) of all heads from the (m, l) partials,
+//                  then w_h = 2^(s_h - M_h) / L_h summed over the heads and
+//                  divided by Hq, optional per-head weights, and the engine's
+//                  decayed score feedback (cache_engine.cpp:511-540).
+// Neither kind waits for the other, so the two run side by side.
+// ---------------------------------------------------------------------------
+struct FinArgs {
+    const float* part_ml;
+    const float* part_acc;
+    int nsplit;
+    int D;
     int Hq;
-    int n_static;  // token count when no engine state
+    float* out;
+    float* rowstat;
+    const float* logits;  // null: no mean-weight workgroups
+    int ld;
+    int n_static;         // token count when no engine state
     const int* state;
     int kgs;
     float* mw;
@@ -489,20 +440,116 @@ struct MeanArgs {
     Feedback fb;
 };
 
-// One thread per attended token, one wave per workgroup so the grid covers
-// every CU: w_h = exp(s_h - max_h) / sum_h summed over h = 0..Hq-1 in order
-// and divided by Hq (fused_attn_avx2.cpp:286-300), then the engine's decayed
-// score feedback for that token (cache_engine.cpp:511-540).
-__global__ void __launch_bounds__(64) attn_mean_kernel(MeanArgs a) {
-    extern __shared__ float sh[];  // [Hq] row max (log2 units), [Hq] 1/sum
-    for (int h = threadIdx.x; h < a.Hq; h += blockDim.x) {
-        const float M = a.rowstat[2 * h];
-        const float L = a.rowstat[2 * h + 1];
-        sh[h] = M;
-        sh[a.Hq + h] = 1.0f / (L > 0.0f ? L : 1.0f);
+// Wave-wide reductions with DPP inside rows and two cross-row swaps.
+__device__ __forceinline__ float wave_max(float x) {
+    x = fmaxf(x, dpp<0xB1>(x));
+    x = fmaxf(x, dpp<0x4E>(x));
+    x = fmaxf(x, dpp<0x141>(x));
+    x = fmaxf(x, dpp<0x140>(x));
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+__device__ __forceinline__ float wave_sum(float x) {
+    x = row_sum16(x);
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
+
+// Merge of query head h. Every load is issued before the first reduction:
+// thread t holds (m_t, l_t) of split t, and thread (group g, channel quad c4)
+// the accumulators of splits g, g + groups, ... (unrolled in batches of 8).
+__device__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const float* ml = a.part_ml + static_cast<size_t>(h) * a.nsplit * 2;
+    const int q = a.D >> 2;
+    const int groups = 256 / q;
+    const int g = t / q, c4 = t - g * q;
+    const float* base = a.part_acc + static_cast<size_t>(h) * a.nsplit * a.D + 4 * c4;
+    float* red = sh + 8;  // [256][4]
+    float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float L = 0.0f, M = kNegInf;
+    for (int j0 = 0; j0 < a.nsplit; j0 += 256) {
+        // (max, sum) over splits j0 .. j0 + 255 folded into the running (M, L)
+        const int jt = j0 + t;
+        const float mt = jt < a.nsplit ? ml[2 * jt] : kNegInf;
+        const float lt = jt < a.nsplit ? ml[2 * jt + 1] : 0.0f;
+        float4 v[8];
+        float mv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int j = j0 + g + u * groups;
+            const bool in = g < groups && j < a.nsplit && j < j0 + 256;
+            v[u] = in ? *reinterpret_cast<const float4*>(base + static_cast<size_t>(j) * a.D)
+                      : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            mv[u] = in ? ml[2 * j] : kNegInf;
+        }
+        const float wm = wave_max(mt);
+        if (lane == 0) sh[wave] = wm;
+        __syncthreads();
+        const float Mb = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+        const float Mn = fmaxf(M, Mb);
+        const float ws = wave_sum(mt == kNegInf ? 0.0f : exp2f(mt - Mn) * lt);
+        __syncthreads();
+        if (lane == 0) sh[4 + wave] = ws;
+        const float al = (M == kNegInf) ? 0.0f : exp2f(M - Mn);
+        A.x *= al; A.y *= al; A.z *= al; A.w *= al;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float f = (mv[u] == kNegInf) ? 0.0f : exp2f(mv[u] - Mn);
+            A.x = __builtin_fmaf(f, v[u].x, A.x);
+            A.y = __builtin_fmaf(f, v[u].y, A.y);
+            A.z = __builtin_fmaf(f, v[u].z, A.z);
+            A.w = __builtin_fmaf(f, v[u].w, A.w);
+        }
+        // splits beyond 8 per group in this block of 256 (only when groups < 32)
+        for (int j = j0 + g + 8 * groups; g < groups && j < a.nsplit && j < j0 + 256; j += groups) {
+            const float mj = ml[2 * j];
+            const float f = (mj == kNegInf) ? 0.0f : exp2f(mj - Mn);
+            const float4 w = *reinterpret_cast<const float4*>(base + static_cast<size_t>(j) * a.D);
+            A.x = __builtin_fmaf(f, w.x, A.x);
+            A.y = __builtin_fmaf(f, w.y, A.y);
+            A.z = __builtin_fmaf(f, w.z, A.z);
+            A.w = __builtin_fmaf(f, w.w, A.w);
+        }
+        __syncthreads();
+        L = L * al + ((sh[4] + sh[5]) + (sh[6] + sh[7]));
+        M = Mn;
+        __syncthreads();
     }
+    *reinterpret_cast<float4*>(red + 4 * t) = A;
     __syncthreads();
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t < a.D) {
+        const int cq = t >> 2, ci = t & 3;
+        float o = 0.0f;
+        for (int gg = 0; gg < groups; ++gg) o += red[4 * (gg * q + cq) + ci];
+        a.out[static_cast<size_t>(h) * a.D + t] = (L > 0.0f) ? o / L : 0.0f;
+    }
+    if (t == 0) {
+        a.rowstat[2 * h] = M;
+        a.rowstat[2 * h + 1] = L;
+    }
+}
+
+// Max over the 8 lanes of an aligned group (xor 1, 2, 4 via DPP).
+__device__ __forceinline__ float max8(float x) {
+    x = fmaxf(x, dpp<0xB1>(x));
+    x = fmaxf(x, dpp<0x4E>(x));
+    return fmaxf(x, dpp<0x141>(x) /* row_half_mirror pairs lanes 0-7 */);
+}
+__device__ __forceinline__ float sum8(float x) {
+    x = x + dpp<0xB1>(x);
+    x = x + dpp<0x4E>(x);
+    return x + dpp<0x141>(x);
+}
+
+__device__ void fin_mean_tokens(const FinArgs& a, const int blk, float* sh) {
+    const int t = threadIdx.x;
+    const int Hq = a.Hq;
     int n = a.n_static;
     int s = 0, hh = 0, rw = 0, total = 0, Nd = 0;
     if (a.state) {
@@ -513,28 +560,104 @@ __global__ void __launch_bounds__(64) attn_mean_kernel(MeanArgs a) {
         Nd = s + hh + rw;
         n = Nd + a.state[kBlocksUsed] * a.kgs;
     }
-    if (i >= n) return;
-    const float* lg = a.logits + i;
-    float sum = 0.0f;
-    int h = 0;
-    for (; h + 8 <= a.Hq; h += 8) {
-        float sc[8];
+    const int tok0 = blk * 256;
+    if (tok0 >= n) return;
+    // Thread (head group hg, token quad q): heads hg, hg + 4, ...; tokens
+    // tok0 + 4 q .. + 3. Rows are padded to a multiple of 4 floats. The
+    // logits of the first 32 heads are loaded before anything else.
+    const int q = t & 63, hg = t >> 6;
+    const int i0 = tok0 + 4 * q;
+    const bool whole = i0 + 4 <= n;
+    float4 lgv[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) sc[u] = lg[static_cast<size_t>(h + u) * a.ld];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const float w = (sc[u] == kNegInf) ? 0.0f : exp2f(sc[u] - sh[h + u]) * sh[a.Hq + h + u];
-            sum += w;
-            if (a.head_w && i < a.head_w_ld) a.head_w[static_cast<size_t>(h + u) * a.head_w_ld + i] = w;
+    for (int u = 0; u < 8; ++u) {
+        const int h = hg + 4 * u;
+        lgv[u] = make_float4(kNegInf, kNegInf, kNegInf, kNegInf);
+        if (h < Hq && i0 < n) {
+            const float* lg = a.logits + static_cast<size_t>(h) * a.ld + i0;
+            if (whole) {
+                lgv[u] = *reinterpret_cast<const float4*>(lg);
+            } else {
+                lgv[u].x = lg[0];
+                if (i0 + 1 < n) lgv[u].y = lg[1];
+                if (i0 + 2 < n) lgv[u].z = lg[2];
+            }
         }
     }
-    for (; h < a.Hq; ++h) {
-        const float sc = lg[static_cast<size_t>(h) * a.ld];
-        const float w = (sc == kNegInf) ? 0.0f : exp2f(sc - sh[h]) * sh[a.Hq + h];
-        sum += w;
-        if (a.head_w && i < a.head_w_ld) a.head_w[static_cast<size_t>(h) * a.head_w_ld + i] = w;
+    // (M_h, 1/L_h) of every head: 8 threads per head, splits j0, j0 + 8, ...
+    float* Mh = sh;        // [Hq]
+    float* iL = sh + Hq;   // [Hq]
+    for (int h0 = 0; h0 < Hq; h0 += 32) {
+        const int h = h0 + (t >> 3), j0 = t & 7;
+        const float* ml = a.part_ml + static_cast<size_t>(h < Hq ? h : 0) * a.nsplit * 2;
+        float mx = kNegInf, ls = 0.0f;
+        for (int jb = j0; jb < a.nsplit; jb += 64) {
+            float mv[8], lv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int j = jb + 8 * u;
+                mv[u] = j < a.nsplit ? ml[2 * j] : kNegInf;
+                lv[u] = j < a.nsplit ? ml[2 * j + 1] : 0.0f;
+            }
+            float bm = kNegInf;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) bm = fmaxf(bm, mv[u]);
+            const float mn = fmaxf(mx, bm);
+            float bs = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) bs += (mv[u] == kNegInf) ? 0.0f : exp2f(mv[u] - mn) * lv[u];
+            ls = ((mx == kNegInf) ? 0.0f : ls * exp2f(mx - mn)) + bs;
+            mx = mn;
+        }
+        const float gm = max8(mx);
+        const float gl = sum8((mx == kNegInf) ? 0.0f : ls * exp2f(mx - gm));
+        if (j0 == 0 && h < Hq) {
+            Mh[h] = gm;
+            iL[h] = 1.0f / (gl > 0.0f ? gl : 1.0f);
+        }
     }
-    const float mean = sum / static_cast<float>(a.Hq);
+    __syncthreads();
+    float w4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (i0 < n) {
+        for (int hb = 0; hb < Hq; hb += 32) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int h = hb + hg + 4 * u;
+                if (h >= Hq) break;
+                float4 v;
+                if (hb == 0) {
+                    v = lgv[u];
+                } else {
+                    const float* lg = a.logits + static_cast<size_t>(h) * a.ld + i0;
+                    v = make_float4(kNegInf, kNegInf, kNegInf, kNegInf);
+                    if (whole) {
+                        v = *reinterpret_cast<const float4*>(lg);
+                    } else {
+                        v.x = lg[0];
+                        if (i0 + 1 < n) v.y = lg[1];
+                        if (i0 + 2 < n) v.z = lg[2];
+                    }
+                }
+                const float sc[4] = {v.x, v.y, v.z, v.w};
+                const float mh = Mh[h], il = iL[h];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float w = (sc[e] == kNegInf) ? 0.0f : exp2f(sc[e] - mh) * il;
+                    w4[e] += w;
+                    if (a.head_w && i0 + e < n && i0 + e < a.head_w_ld)
+                        a.head_w[static_cast<size_t>(h) * a.head_w_ld + i0 + e] = w;
+                }
+            }
+        }
+    }
+    float* red = sh + 2 * Hq;  // [4][256]
+#pragma unroll
+    for (int e = 0; e < 4; ++e) red[hg * 256 + 4 * q + e] = w4[e];
+    __syncthreads();
+    const int i = tok0 + t;
+    if (i >= n) return;
+    const float sum = (red[t] + red[256 + t]) + (red[512 + t] + red[768 + t]);
+    const float mean = sum / static_cast<float>(Hq);
     if (a.mw) a.mw[i] = mean;
     if (a.fb.g) {
         long long tid;
@@ -555,6 +678,15 @@ __global__ void __launch_bounds__(64) attn_mean_kernel(MeanArgs a) {
             if (hh_slot >= 0) a.fb.hh_scores[hh_slot] = gn;
         }
     }
+}
+
+__global__ void __launch_bounds__(256) attn_finalize_kernel(FinArgs a) {
+    extern __shared__ float sh[];
+    const int b = static_cast<int>(blockIdx.x);
+    if (b < a.Hq)
+        fin_merge_head(a, b, sh);
+    else
+        fin_mean_tokens(a, b - a.Hq, sh);
 }
 
 template <int CPL, int GP>
@@ -578,21 +710,21 @@ int launch_split_g(const SplitArgs& a, dim3 grid, int gp, int meta_fp16, hipStre
 }
 
 template <int GP>
-int launch_tiles_meta(const SplitArgs& a, dim3 grid, int meta_fp16, hipStream_t st) {
+int launch_packed_meta(const SplitArgs& a, dim3 grid, int meta_fp16, hipStream_t st) {
     if (meta_fp16)
-        hipLaunchKernelGGL((attn_tiles_kernel<GP, uint16_t>), grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((attn_packed_kernel<GP, uint16_t>), grid, dim3(256), 0, st, a);
     else
-        hipLaunchKernelGGL((attn_tiles_kernel<GP, float>), grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((attn_packed_kernel<GP, float>), grid, dim3(256), 0, st, a);
     TT_LAUNCH_CHECK();
     return TT_OK;
 }
 
-int launch_tiles(const SplitArgs& a, dim3 grid, int gp, int meta_fp16, hipStream_t st) {
+int launch_packed(const SplitArgs& a, dim3 grid, int gp, int meta_fp16, hipStream_t st) {
     switch (gp) {
-    case 1: return launch_tiles_meta<1>(a, grid, meta_fp16, st);
-    case 2: return launch_tiles_meta<2>(a, grid, meta_fp16, st);
-    case 4: return launch_tiles_meta<4>(a, grid, meta_fp16, st);
-    default: return launch_tiles_meta<8>(a, grid, meta_fp16, st);
+    case 1: return launch_packed_meta<1>(a, grid, meta_fp16, st);
+    case 2: return launch_packed_meta<2>(a, grid, meta_fp16, st);
+    case 4: return launch_packed_meta<4>(a, grid, meta_fp16, st);
+    default: return launch_packed_meta<8>(a, grid, meta_fp16, st);
     }
 }
 
@@ -601,15 +733,15 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 int gp_for(int G) { return G >= 8 ? 8 : (G > 4 ? 8 : (G > 2 ? 4 : G)); }
 
 // The matrix-core path serves head_dim 128 with either block size.
-bool use_tiles_kernel(int D) { return D == kMfD; }
+bool use_packed_kernel(int D) { return D == kMfD; }
 
 template <typename MetaT>
-const void* tiles_kernel_ptr(int gp) {
+const void* packed_kernel_ptr(int gp) {
     switch (gp) {
-    case 1: return reinterpret_cast<const void*>(&attn_tiles_kernel<1, MetaT>);
-    case 2: return reinterpret_cast<const void*>(&attn_tiles_kernel<2, MetaT>);
-    case 4: return reinterpret_cast<const void*>(&attn_tiles_kernel<4, MetaT>);
-    default: return reinterpret_cast<const void*>(&attn_tiles_kernel<8, MetaT>);
+    case 1: return reinterpret_cast<const void*>(&attn_packed_kernel<1, MetaT>);
+    case 2: return reinterpret_cast<const void*>(&attn_packed_kernel<2, MetaT>);
+    case 4: return reinterpret_cast<const void*>(&attn_packed_kernel<4, MetaT>);
+    default: return reinterpret_cast<const void*>(&attn_packed_kernel<8, MetaT>);
     }
 }
 
@@ -642,8 +774,8 @@ int resident_split_wgs(int D, int G, int fp16) {
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     const void* fn = nullptr;
-    if (use_tiles_kernel(D)) {
-        fn = fp16 ? tiles_kernel_ptr<uint16_t>(gp) : tiles_kernel_ptr<float>(gp);
+    if (use_packed_kernel(D)) {
+        fn = fp16 ? packed_kernel_ptr<uint16_t>(gp) : packed_kernel_ptr<float>(gp);
     } else {
         switch (D) {
         case 16: fn = split_kernel_ptr<1>(gp, fp16); break;
@@ -683,14 +815,13 @@ AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs,
     const long long resident = resident_split_wgs(D, G, meta_fp16);
     const long long per_head = std::max<long long>(1, (resident + heads - 1) / heads);
     const long long dense_tiles = (dense_ub + 15) / 16;
-    if (use_tiles_kernel(D)) {
-        // Dense workgroups take ~8 FP32 tiles (two per wave); the packed
-        // workgroups fill the rest of one resident round, with at least ~8
-        // pairs of tiles each so the partials stay small.
+    if (use_packed_kernel(D)) {
+        // One resident round of workgroups, each with at least ~8 pairs of
+        // packed tiles (or 2 FP32 tiles) so the partials stay small.
         const long long pairs = (static_cast<long long>(blocks_ub) * W + 1) / 2;
-        p.nsplit_d = static_cast<int>(std::max<long long>(1, (dense_tiles + 7) / 8));
-        const long long want = std::max<long long>(1, per_head - p.nsplit_d);
-        p.nsplit_p = static_cast<int>(std::max<long long>(1, std::min(want, pairs / 8)));
+        const long long work = std::max(pairs / 8, dense_tiles / 2);
+        p.nsplit_d = 0;
+        p.nsplit_p = static_cast<int>(std::max<long long>(1, std::min(per_head, work)));
     } else {
         // One round of resident workgroups, but at least ~32 packed-tile
         // units of work per workgroup so the merge traffic stays small.
@@ -728,16 +859,16 @@ int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipS
     a.nsplit = plan.nsplit;
     a.nsplit_p = plan.nsplit_p;
     a.nsplit_d = plan.nsplit_d;
-    a.dense_only = plan.nsplit_p > 0 ? 1 : 0;
     a.wd = 8;
     a.wp = 1;
     const int G = in.Hq / in.Hkv;
     const int gp = gp_for(G);
-    const dim3 grid(plan.nsplit, in.Hkv, (G + gp - 1) / gp);
-    if (use_tiles_kernel(in.D)) {
-        if (plan.nsplit_p <= 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
-        return launch_tiles(a, grid, gp, in.meta_fp16, stream);
+    const int chunks = (G + gp - 1) / gp;
+    if (use_packed_kernel(in.D)) {
+        if (plan.nsplit_p <= 0 || plan.nsplit_d != 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
+        return launch_packed(a, dim3(plan.nsplit_p, in.Hkv, chunks), gp, in.meta_fp16, stream);
     }
+    const dim3 grid(plan.nsplit, in.Hkv, chunks);
     if (plan.nsplit_p != 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
     switch (in.D) {
     case 16: return launch_split_g<1>(a, grid, gp, in.meta_fp16, stream);
@@ -751,30 +882,28 @@ int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipS
 int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out, float* mean_w,
                          const Feedback* fb, float* head_w, int head_w_ld, hipStream_t stream) {
     char* base = static_cast<char*>(ws);
-    const float* part_ml = reinterpret_cast<const float*>(base + plan.off_ml);
-    const float* part_acc = reinterpret_cast<const float*>(base + plan.off_acc);
-    float* rowstat = reinterpret_cast<float*>(base + plan.off_rowstat);
-    const size_t merge_lds = sizeof(float) * (static_cast<size_t>(plan.nsplit) + 256);
-    hipLaunchKernelGGL(attn_merge_kernel, dim3(in.Hq), dim3(256), merge_lds, stream, part_ml, part_acc, plan.nsplit,
-                       in.D, out, rowstat);
+    FinArgs f;
+    f.part_ml = reinterpret_cast<const float*>(base + plan.off_ml);
+    f.part_acc = reinterpret_cast<const float*>(base + plan.off_acc);
+    f.nsplit = plan.nsplit;
+    f.D = in.D;
+    f.Hq = in.Hq;
+    f.out = out;
+    f.rowstat = reinterpret_cast<float*>(base + plan.off_rowstat);
+    const bool weights = plan.logits && (mean_w || head_w || (fb && fb->g));
+    f.logits = weights ? reinterpret_cast<const float*>(base + plan.off_logits) : nullptr;
+    f.ld = plan.ld;
+    f.n_static = in.n0 + in.n1 + in.n2 + in.num_blocks * in.kgs;
+    f.state = in.state;
+    f.kgs = in.kgs;
+    f.mw = mean_w;
+    f.head_w = head_w;
+    f.head_w_ld = head_w_ld;
+    f.fb = fb ? *fb : Feedback{};
+    const int mean_wgs = weights ? (std::max(plan.token_ub, 1) + 255) / 256 : 0;
+    const size_t lds = sizeof(float) * std::max<size_t>(8 + 4 * 256, 2 * static_cast<size_t>(in.Hq) + 4 * 256);
+    hipLaunchKernelGGL(attn_finalize_kernel, dim3(in.Hq + mean_wgs), dim3(256), lds, stream, f);
     TT_LAUNCH_CHECK();
-    if (plan.logits && (mean_w || head_w || (fb && fb->g))) {
-        MeanArgs m;
-        m.logits = reinterpret_cast<const float*>(base + plan.off_logits);
-        m.ld = plan.ld;
-        m.rowstat = rowstat;
-        m.Hq = in.Hq;
-        m.n_static = in.n0 + in.n1 + in.n2 + in.num_blocks * in.kgs;
-        m.state = in.state;
-        m.kgs = in.kgs;
-        m.mw = mean_w;
-        m.head_w = head_w;
-        m.head_w_ld = head_w_ld;
-        m.fb = fb ? *fb : Feedback{};
-        const int n = std::max(plan.token_ub, 1);
-        hipLaunchKernelGGL(attn_mean_kernel, dim3((n + 63) / 64), dim3(64), sizeof(float) * 2 * in.Hq, stream, m);
-        TT_LAUNCH_CHECK();
-    }
     return TT_OK;
 }
 

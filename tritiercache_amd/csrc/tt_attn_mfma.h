@@ -54,16 +54,38 @@ struct MfLds {
     static constexpr int KT = 0;       // [2 tiles][4 token quads][128 channel bytes]
     static constexpr int VT = 1024;    // [32 byte columns][32 token bytes in MFMA order]
     static constexpr int KSZ = 2048;   // [2 tiles][scale | zero][128] f32
-    static constexpr int VS = 4096;    // [32] f32, MFMA token order
+    static constexpr int VS = 4096;    // [32] f32, MFMA token order (0 for masked slots)
     static constexpr int VZ = 4224;    // [32] f32
-    static constexpr int BIAS = 4352;  // [16] f32 per-head QK bias
-    static constexpr int BHI = 4416;   // [GP][128] f16 QK coefficients, MFMA channel order
-    static constexpr int BLO = BHI + GP * 2 * kMfD;
-    static constexpr int BYTES = BLO + GP * 2 * kMfD;
+    static constexpr int BIAS = 4352;  // [2 tiles][8] f32 per-head QK bias
+    static constexpr int BHL = 4416;   // [2 tiles][hi rows 0..GP-1, lo rows GP..2GP-1][128] f16
+    static constexpr int BHL_TILE = 2 * GP * kMfD * 2;
+    static constexpr int BYTES = BHL + 2 * BHL_TILE;
     // final merge of the four waves, reusing the staging area
     static constexpr int MERGE = 4 * GP * (3 + kMfD) * 4;
     static_assert(MERGE <= 4 * BYTES, "merge area must fit in the staging area");
+    // per-wave dense partials [4][GP][max, sum, acc[128]], after the four staging areas
+    static constexpr int DENSE = 4 * BYTES;
+    static constexpr int TOTAL = DENSE + 4 * GP * (2 + kMfD) * 4;
 };
+
+// Reductions over the four 16-lane rows of a wave (lanes n, n+16, n+32, n+48).
+__device__ __forceinline__ float xrow_max(float x) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+}
+__device__ __forceinline__ float xrow_sum(float x) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(s[0]) + __uint_as_float(s[1]);
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
+// x[l] + x[l ^ 32]
+__device__ __forceinline__ float xhalf_sum(float x) {
+    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
 
 __device__ __forceinline__ float row_max16(float x) {
     x = fmaxf(x, dpp<0xB1>(x));
@@ -95,8 +117,10 @@ __device__ __forceinline__ mf_f4 mfma16x16x32(mf_u4 a, mf_u4 b, mf_f4 c) {
 
 // Two 2-bit codes of x at bit offsets 2k and 16 + 2k (mk selects them) ->
 // the f16 pair (q0 4^k, q1 4^k), exact.
-__device__ __forceinline__ uint32_t code_f16(uint32_t x, uint32_t mk) {
-    const mf_h2 v = __builtin_bit_cast(mf_h2, (x & mk) | 0x64006400u);
+// `one024` holds 0x64006400 in a VGPR: v_and_or_b32 may read only one SGPR
+// (the mask) on this target, so a second scalar constant would split it in two.
+__device__ __forceinline__ uint32_t code_f16(uint32_t x, uint32_t mk, uint32_t one024) {
+    const mf_h2 v = __builtin_bit_cast(mf_h2, (x & mk) | one024);
     const mf_h2 off = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
     return __builtin_bit_cast(uint32_t, v - off);
 }
@@ -132,11 +156,176 @@ __device__ __forceinline__ float4 load_meta4(const MetaT* __restrict__ p) {
     }
 }
 
+// Even split of `count` items over `parts`: the first item of part `i`
+// (32-bit unsigned arithmetic: count * i stays below 2^32 for every
+// supported size, and a 64-bit divide is a long software loop).
+__device__ __forceinline__ int part_begin(const int count, const int i, const int parts) {
+    // The divide is expanded into vector instructions; readfirstlane hands the
+    // (wave-uniform) result back to the scalar unit so loop bounds and the
+    // branches that depend on them stay uniform.
+    return __builtin_amdgcn_readfirstlane(
+        static_cast<int>(static_cast<unsigned>(count) * static_cast<unsigned>(i) / static_cast<unsigned>(parts)));
+}
+
+// FP32 16-token tiles of workgroup `split` (its share of the dense tiers).
+__device__ __forceinline__ void dense_range(const SplitArgs& a, const int split, int& d0, int& d1) {
+    const AttnInputs& in = a.in;
+    int Nd = in.n0 + in.n1 + in.n2;
+    if (in.state) Nd = in.state[kSCount] + in.state[kHhCount] + in.state[kRwCount];
+    const int Td = (Nd + 15) >> 4;
+    d0 = part_begin(Td, split, a.nsplit_p);
+    d1 = part_begin(Td, split + 1, a.nsplit_p);
+}
+
+// FP32 tiers of the workgroup's share (16-token tiles [d0, d1) of the logical
+// dense order sinks -> heavy hitters -> recent ring), VALU, before the packed
+// loop. Wave w takes tiles d0 + w, d0 + w + 4, ...; lanes are (token group tg
+// = lane / 16) x (8-channel slice cp = lane % 16), the query heads of the
+// group in passes of up to four. Leaves one (max, sum, acc[128]) partial per
+// head in `dl` ([GP][2 + 128] per wave) and writes the dense logits.
+template <int GP>
+__device__ __forceinline__ void dense_share(const SplitArgs& a, const int split, const int kvh, const int g0,
+                                            const int gc, const int wave, float* dl) {
+    constexpr int HP = GP < 4 ? GP : 4;
+    constexpr int NPASS = GP / HP;
+    const AttnInputs& in = a.in;
+    const int lane = threadIdx.x & 63;
+    const int tg = lane >> 4, cp = lane & 15;
+    const int G = in.Hq / in.Hkv;
+    const int Hkv = in.Hkv;
+    int n0 = in.n0, n1 = in.n1, n2 = in.n2, head = in.ring_head;
+    if (in.state) {
+        n0 = in.state[kSCount];
+        n1 = in.state[kHhCount];
+        n2 = in.state[kRwCount];
+        head = in.state[kRwHead];
+    }
+    const int Nd = n0 + n1 + n2;
+    int d0, d1;
+    dense_range(a, split, d0, d1);
+    float* my = dl + wave * GP * (2 + kMfD);
+#pragma unroll 1
+    for (int pass = 0; pass < NPASS; ++pass) {
+        const int gb = pass * HP;
+        float q[HP][8];
+#pragma unroll
+        for (int g = 0; g < HP; ++g) {
+            if (gb + g < gc) {
+                load_f32<8>(in.Q + static_cast<size_t>(kvh * G + g0 + gb + g) * kMfD + cp * 8, q[g]);
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) q[g][j] = 0.0f;
+            }
+        }
+        float m[HP], l[HP], acc[HP][8];
+#pragma unroll
+        for (int g = 0; g < HP; ++g) {
+            m[g] = kNegInf;
+            l[g] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
+        }
+        for (int k = d0 + wave; k < d1; k += 4) {
+            const int tok0 = 16 * k + 4 * tg;
+            float kx[4][8], vx[4][8];
+            bool valid[4];
+            // Rows past the tiers repeat the last row (finite data, masked below).
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r0 = tok0 + i;
+                valid[i] = r0 < Nd;
+                const int r = valid[i] ? r0 : Nd - 1;
+                const bool in0 = r < n0, in1 = r < n0 + n1;
+                int ring = head + (r - n0 - n1);
+                ring = ring >= in.ring_size ? ring - in.ring_size : ring;
+                const int idx = in0 ? r : (in1 ? r - n0 : ring);
+                const float* kb = in0 ? in.k0 : (in1 ? in.k1 : in.k2);
+                const float* vb = in0 ? in.v0 : (in1 ? in.v1 : in.v2);
+                const int off = (idx * Hkv + kvh) * kMfD + cp * 8;
+                load_f32<8>(kb + off, kx[i]);
+                load_f32<8>(vb + off, vx[i]);
+            }
+            float s[4][HP];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int g = 0; g < HP; ++g) {
+                    float d = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) d = __builtin_fmaf(q[g][j], kx[i][j], d);
+                    const float t = row_sum16(d) * a.scale2;
+                    s[i][g] = valid[i] ? t : kNegInf;
+                }
+            if (a.logits) {
+#pragma unroll
+                for (int g = 0; g < HP; ++g) {
+                    if (gb + g < gc && cp == g) {
+                        float* lr = a.logits + static_cast<size_t>(kvh * G + g0 + gb + g) * a.ld + tok0;
+                        if (tok0 + 4 <= Nd) {
+                            *reinterpret_cast<float4*>(lr) = make_float4(s[0][g], s[1][g], s[2][g], s[3][g]);
+                        } else {
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                if (valid[i]) lr[i] = s[i][g];
+                        }
+                    }
+                }
+            }
+#pragma unroll
+            for (int g = 0; g < HP; ++g) {
+                float tm = fmaxf(fmaxf(s[0][g], s[1][g]), fmaxf(s[2][g], s[3][g]));
+                tm = xrow_max(tm);
+                const float mn = fmaxf(m[g], tm);
+                const float alpha = (m[g] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(m[g] - mn);
+                float p[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) p[i] = (s[i][g] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(s[i][g] - mn);
+                l[g] = __builtin_fmaf(l[g], alpha, (p[0] + p[1]) + (p[2] + p[3]));
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float v = acc[g][j] * alpha;
+                    v = __builtin_fmaf(p[0], vx[0][j], v);
+                    v = __builtin_fmaf(p[1], vx[1][j], v);
+                    v = __builtin_fmaf(p[2], vx[2][j], v);
+                    v = __builtin_fmaf(p[3], vx[3][j], v);
+                    acc[g][j] = v;
+                }
+                m[g] = mn;
+            }
+        }
+        // Sum the four row groups (they share m) and leave the partial in LDS.
+#pragma unroll
+        for (int g = 0; g < HP; ++g) {
+            const float lt = xrow_sum(l[g]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[g][j] = xrow_sum(acc[g][j]);
+            if (gb + g < GP && tg == 0) {
+                float* pg = my + (gb + g) * (2 + kMfD);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) pg[2 + cp * 8 + j] = acc[g][j];
+                if (cp == 0) {
+                    pg[0] = m[g];
+                    pg[1] = lt;
+                }
+            }
+        }
+    }
+}
+
 // One workgroup: KV head blockIdx.y, query heads [GP * blockIdx.z, +GP), a
-// contiguous range of 32-token pairs of packed tiles; wave w takes pairs
-// w, w + 4, ... of the range. Writes partial slot `split` of each head.
+// contiguous range of 32-token pairs of packed tiles and a share of the FP32
+// tiles; each wave takes a contiguous sub-range of the pairs. Writes partial
+// slot `split` of each head.
+//
+// The high and low f16 halves of the QK coefficients sit in MFMA columns
+// h and h + 8, so one MFMA per 32 channels yields both products; a DPP
+// row rotation by 8 adds them, after which columns h and h + 8 carry the same
+// logits and run the same softmax. The PV operand likewise puts p vs high in
+// row h and low in row h + 8; the two accumulator rows are added once at the
+// end. Columns / rows of padding heads repeat head 0 and are never stored.
 template <int GP, typename MetaT>
 __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split, char* lds) {
+    static_assert(GP >= 1 && GP <= 8, "at most 8 query heads per workgroup");
     constexpr int NP = GP >= 4 ? GP / 4 : 1;  // coefficient passes (4 heads x 16 chunks each)
     using L = MfLds<GP>;
     const AttnInputs& in = a.in;
@@ -145,9 +334,11 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     const int g0 = blockIdx.z * GP;
     const int gc = min(GP, G - g0);
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int n = lane & 15;   // MFMA column: query head (QK) / channel group (PV); chunk of 8 channels (coefficients)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loop control
+    const int n = lane & 15;   // MFMA column (QK) / channel group (PV); chunk of 8 channels (coefficients)
     const int gk = lane >> 4;  // MFMA reduction group
+    const int hn = n & 7;      // query head of column n
+    const bool lo_col = n >= 8;
     const int Hkv = in.Hkv;
 
     int n0 = in.n0, n1 = in.n1, n2 = in.n2, nb = in.num_blocks;
@@ -162,8 +353,10 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     const int Tp = nb * W;           // 16-token tiles
     const int nslots = nb * in.kgs;  // packed token slots
     const int P = (Tp + 1) >> 1;     // 32-token pairs
-    const int pb = static_cast<int>(static_cast<long long>(P) * split / a.nsplit_p);
-    const int pe = static_cast<int>(static_cast<long long>(P) * (split + 1) / a.nsplit_p);
+    const int pb = part_begin(P, split, a.nsplit_p);
+    const int pe = part_begin(P, split + 1, a.nsplit_p);
+    const int tstride = Hkv * kMfD;         // words (or meta entries) between tiles / blocks of one head
+    const int vstride = Hkv * (kMfD / 16);  // V words between tokens
 
     char* wl = lds + wave * L::BYTES;
     uint32_t* kt_l = reinterpret_cast<uint32_t*>(wl + L::KT);
@@ -172,8 +365,12 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     float* vs_l = reinterpret_cast<float*>(wl + L::VS);
     float* vz_l = reinterpret_cast<float*>(wl + L::VZ);
     float* bias_l = reinterpret_cast<float*>(wl + L::BIAS);
-    char* bhi_l = wl + L::BHI;
-    char* blo_l = wl + L::BLO;
+    char* bhl_l = wl + L::BHL;
+
+    // The workgroup's share of the FP32 tiers first, before the packed loop's
+    // registers are live.
+    float* dl = reinterpret_cast<float*>(lds + L::DENSE);
+    dense_share<GP>(a, split, kvh, g0, gc, wave, dl);
 
     // Q' = Q 2^-e per head (e = exponent of max |Q_h|) in the coefficient
     // layout: pass pp, head 4 pp + gk, channels 8 n .. 8 n + 7.
@@ -201,52 +398,63 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         for (int j = 0; j < 8; ++j) qv[pp][j] = __builtin_amdgcn_ldexpf(qv[pp][j], -e);
         cpass[pp] = (h < gc) ? __builtin_amdgcn_ldexpf(a.scale2, e) : 0.0f;
     }
-    // Column scale of query head n: lane 16 (n & 3) of pass n >> 2 holds it.
+    // Column scale of query head hn: lane 16 (hn & 3) of pass hn >> 2 holds it.
     float ccol = 0.0f;
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
-        const float t = __shfl(cpass[pp], 16 * (n & 3), 64);
-        if ((n >> 2) == pp) ccol = t;
+        const float t = __shfl(cpass[pp], 16 * (hn & 3), 64);
+        if ((hn >> 2) == pp) ccol = t;
     }
     float crow[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) crow[r] = __builtin_amdgcn_ldexpf(ccol, -2 * r);
+    const int bhead = hn < GP ? hn : 0;
+    const int brow = bhead + (lo_col ? GP : 0);
 
     const uint32_t kmask = (3u << (2 * (lane & 3))) | (3u << (16 + 2 * (lane & 3)));
+    uint32_t one024;
+    asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(one024));
     const uint32_t qsel1 = (lane & 1) ? 0x03070105u : 0x06020400u;
     const uint32_t qsel2 = (lane & 2) ? 0x03020706u : 0x05040100u;
 
-    const MetaT* ks = static_cast<const MetaT*>(in.ks);
-    const MetaT* kz = static_cast<const MetaT*>(in.kz);
-    const MetaT* vs = static_cast<const MetaT*>(in.vs);
-    const MetaT* vz = static_cast<const MetaT*>(in.vz);
+    const int32_t* kp_h = in.kp + kvh * kMfD;
+    const MetaT* ks_h = static_cast<const MetaT*>(in.ks) + kvh * kMfD;
+    const MetaT* kz_h = static_cast<const MetaT*>(in.kz) + kvh * kMfD;
+    const int32_t* vp_h = in.vp + kvh * (kMfD / 16);
+    const MetaT* vm_h = static_cast<const MetaT*>(lane < 32 ? in.vs : in.vz) + kvh;
+    const int lk = 4 * (lane & 31);
+    const int tv = 4 * (lane >> 3) + (lane & 3);
+    const int hfo = 4 * ((lane >> 2) & 1);
+    const int t2 = lane & 31;
 
     mf_f4 acc[8];
 #pragma unroll
     for (int s = 0; s < 8; ++s) acc[s] = mf_f4{0.0f, 0.0f, 0.0f, 0.0f};
-    float m_run = kNegInf, l_run = 0.0f, pz = 0.0f;
+    float m_run = -1.0e30f, l_run = 0.0f, pz = 0.0f;
 
     // Registers of the pair being fetched.
     mf_u4 kw, vw;
     float4 ksr, kzr;
     float vm = 0.0f;
     long long idv = -1;
+    bool okv = false;
 
     auto fetch = [&](const int p) {
-        const int kt = min(2 * p + (lane >> 5), Tp - 1);
-        const int bk = (W == 2) ? (kt >> 1) : kt;
-        kw = *reinterpret_cast<const mf_u4*>(in.kp + (static_cast<size_t>(kt) * Hkv + kvh) * kMfD + 4 * (lane & 31));
-        const size_t mo = (static_cast<size_t>(bk) * Hkv + kvh) * kMfD + 4 * (lane & 31);
-        ksr = load_meta4<MetaT>(ks + mo);
-        kzr = load_meta4<MetaT>(kz + mo);
-        const int sv = min(32 * p + 4 * (lane >> 3) + (lane & 3), nslots - 1);
-        vw = *reinterpret_cast<const mf_u4*>(in.vp + (static_cast<size_t>(sv) * Hkv + kvh) * (kMfD / 16) +
-                                             4 * ((lane >> 2) & 1));
-        const int sm = min(32 * p + (lane & 31), nslots - 1);
-        vm = Meta<MetaT>::load(lane < 32 ? vs : vz, static_cast<size_t>(sm) * Hkv + kvh);
-        const int si = 32 * p + lane;
-        idv = -1;
-        if (lane < 32 && si < nslots) idv = in.ids[si];
+        const int kt0 = 2 * p;
+        const int kto = min(lane >> 5, Tp - 1 - kt0);  // 0 when the pair has a single tile
+        kw = *reinterpret_cast<const mf_u4*>(kp_h + static_cast<size_t>(kt0) * tstride + (kto * tstride + lk));
+        const int bb = (W == 2) ? p : kt0;
+        const int bo = (W == 2) ? 0 : kto;
+        const size_t mb = static_cast<size_t>(bb) * tstride;
+        ksr = load_meta4<MetaT>(ks_h + mb + (bo * tstride + lk));
+        kzr = load_meta4<MetaT>(kz_h + mb + (bo * tstride + lk));
+        const int s0 = 32 * p;
+        const int lim = nslots - 1 - s0;
+        vw = *reinterpret_cast<const mf_u4*>(vp_h + static_cast<size_t>(s0) * vstride + (min(tv, lim) * vstride + hfo));
+        const int ts = min(t2, lim);
+        vm = Meta<MetaT>::load(vm_h + static_cast<size_t>(s0) * Hkv, static_cast<size_t>(ts * Hkv));
+        idv = in.ids[s0 + ts];
+        okv = t2 <= lim;
     };
 
     // Lays the fetched pair out in LDS; returns the token-validity mask.
@@ -273,92 +481,107 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
             const uint32_t y = __builtin_amdgcn_perm(dpp_u32_quad2(t), t, qsel2);
             vd[g * 32] = y;  // byte column 4 (4 hf + g) + (lane & 3)
         }
-        float* kzd = ksz_l + (lane >> 5) * 256 + 4 * (lane & 31);
+        float* kzd = ksz_l + (lane >> 5) * 256 + lk;
         *reinterpret_cast<float4*>(kzd) = ksr;
         *reinterpret_cast<float4*>(kzd + 128) = kzr;
-        const int t2 = lane & 31;
+        const bool ok = okv && idv != -1;
         const int pos = 8 * ((t2 & 15) >> 2) + 4 * (t2 >> 4) + (t2 & 3);
-        (lane < 32 ? vs_l : vz_l)[pos] = vm;
-        return static_cast<uint32_t>(__ballot(idv != -1));
+        (lane < 32 ? vs_l : vz_l)[pos] = ok ? vm : 0.0f;  // masked slots contribute nothing
+        return static_cast<uint32_t>(__ballot(ok));
     };
 
-    int p = pb + wave;
-    if (p < pe) fetch(p);
-    for (; p < pe; p += 4) {
+    // QK coefficients of one tile's block: hi in rows h, lo in rows GP + h.
+    auto coeffs = [&](const int tile) {
+        char* bt = bhl_l + tile * L::BHL_TILE;
+#pragma unroll
+        for (int pp = 0; pp < NP; ++pp) {
+            const int h = 4 * pp + gk;
+            const float* kss = ksz_l + tile * 256 + 8 * n;
+            const float4 sa = *reinterpret_cast<const float4*>(kss);
+            const float4 sb = *reinterpret_cast<const float4*>(kss + 4);
+            const float4 za = *reinterpret_cast<const float4*>(kss + 128);
+            const float4 zb = *reinterpret_cast<const float4*>(kss + 132);
+            const float sc[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
+            const float zc[8] = {za.x, za.y, za.z, za.w, zb.x, zb.y, zb.z, zb.w};
+            float av[8];
+            float bp = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                av[j] = qv[pp][j] * sc[j];
+                bp = __builtin_fmaf(qv[pp][j], zc[j], bp);
+            }
+            mf_u4 hi, lo;
+            split_hl4(av[0], av[2], av[1], av[3], av[4], av[6], av[5], av[7], hi, lo);
+            bp = row_sum16(bp);
+            if (GP >= 4 || h < GP) {
+                *reinterpret_cast<mf_u4*>(bt + (h * kMfD + 8 * n) * 2) = hi;
+                *reinterpret_cast<mf_u4*>(bt + ((GP + h) * kMfD + 8 * n) * 2) = lo;
+                if (n == 0) bias_l[tile * 8 + h] = bp;
+            }
+        }
+    };
+
+    // Contiguous pair range of this wave: the wave's FP32 tiles (round-robin,
+    // ~kDenseCost pairs each) plus its pairs even out over the four waves.
+    int wp0 = pb, wp1 = pe;
+    {
+        constexpr int kDenseCost = 3;
+        int d0, d1;
+        dense_range(a, split, d0, d1);
+        const int nd = d1 - d0;
+        const int np = pe - pb;
+        // budgets of waves [0, wave) and of this wave (no indexed arrays:
+        // the compiler would move one into LDS per thread)
+        int before = 0, mine = 0, S = 0;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int cd = nd > v ? (nd - v + 3) / 4 : 0;
+            const int share = (nd * kDenseCost + np + 3 - v) / 4;
+            const int b = max(0, share - cd * kDenseCost);
+            before += (v < wave) ? b : 0;
+            mine = (v == wave) ? b : mine;
+            S += b;
+        }
+        if (S > 0) {
+            wp0 = pb + part_begin(np, before, S);
+            wp1 = pb + part_begin(np, before + mine, S);
+        } else {
+            wp0 = wave == 3 ? pb : pe;
+        }
+    }
+    int p = wp0;
+    if (p < wp1) fetch(p);
+    for (; p < wp1; ++p) {
         const uint32_t vmask = stage();
-        if (p + 4 < pe) fetch(p + 4);
+        if (p + 1 < wp1) fetch(p + 1);
         wave_lds_sync();
-        const bool full = (vmask == 0xffffffffu);
+        coeffs(0);
+        if (W == 1) coeffs(1);
+        wave_lds_sync();
 
         float s2[2][4];
 #pragma unroll
         for (int tile = 0; tile < 2; ++tile) {
-            if (tile == 0 || W == 1) {
-                // QK coefficients of this tile's block, MFMA channel order.
-#pragma unroll
-                for (int pp = 0; pp < NP; ++pp) {
-                    const int h = 4 * pp + gk;
-                    const float* kss = ksz_l + tile * 256 + 8 * n;
-                    const float4 sa = *reinterpret_cast<const float4*>(kss);
-                    const float4 sb = *reinterpret_cast<const float4*>(kss + 4);
-                    const float4 za = *reinterpret_cast<const float4*>(kss + 128);
-                    const float4 zb = *reinterpret_cast<const float4*>(kss + 132);
-                    const float sc[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
-                    const float zc[8] = {za.x, za.y, za.z, za.w, zb.x, zb.y, zb.z, zb.w};
-                    float av[8];
-                    float bp = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        av[j] = qv[pp][j] * sc[j];
-                        bp = __builtin_fmaf(qv[pp][j], zc[j], bp);
-                    }
-                    mf_u4 hi, lo;
-                    split_hl4(av[0], av[2], av[1], av[3], av[4], av[6], av[5], av[7], hi, lo);
-                    bp = row_sum16(bp);
-                    if (h < GP) {
-                        *reinterpret_cast<mf_u4*>(bhi_l + (h * kMfD + 8 * n) * 2) = hi;
-                        *reinterpret_cast<mf_u4*>(blo_l + (h * kMfD + 8 * n) * 2) = lo;
-                        if (n == 0) bias_l[h] = bp;
-                    }
-                }
-                wave_lds_sync();
-            }
+            const int tb = (W == 2) ? 0 : tile;
             // A: codes of token t = lane & 15 (k = t & 3), channels 32 gk .. 32 gk + 31.
             const mf_u4* ka = reinterpret_cast<const mf_u4*>(kt_l + (tile * 4 + ((lane & 15) >> 2)) * 32 + 8 * gk);
             const mf_u4 ra = ka[0], rb = ka[1];
-            mf_u4 bh[4], bl[4];
-            float bias = 0.0f;
-            if (n < GP) {
-                const mf_u4* ph = reinterpret_cast<const mf_u4*>(bhi_l + (n * kMfD + 32 * gk) * 2);
-                const mf_u4* pl = reinterpret_cast<const mf_u4*>(blo_l + (n * kMfD + 32 * gk) * 2);
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    bh[s] = ph[s];
-                    bl[s] = pl[s];
-                }
-                bias = bias_l[n];
-            } else {
-#pragma unroll
-                for (int s = 0; s < 4; ++s) {
-                    bh[s] = mf_u4{0u, 0u, 0u, 0u};
-                    bl[s] = mf_u4{0u, 0u, 0u, 0u};
-                }
-            }
+            const mf_u4* kb = reinterpret_cast<const mf_u4*>(bhl_l + tb * L::BHL_TILE + (brow * kMfD + 32 * gk) * 2);
             mf_f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 const uint32_t x = (s < 2) ? ra[2 * s] : rb[2 * s - 4];
                 const uint32_t y = (s < 2) ? ra[2 * s + 1] : rb[2 * s - 3];
-                const mf_u4 av = {code_f16(x, kmask), code_f16(x >> 8, kmask), code_f16(y, kmask),
-                                  code_f16(y >> 8, kmask)};
-                d = mfma16x16x32(av, bh[s], d);
-                d = mfma16x16x32(av, bl[s], d);
+                const mf_u4 av = {code_f16(x, kmask, one024), code_f16(x >> 8, kmask, one024),
+                                  code_f16(y, kmask, one024), code_f16(y >> 8, kmask, one024)};
+                d = mfma16x16x32(av, kb[s], d);
             }
-            const float bc = bias * ccol;
+            const float bc = bias_l[tb * 8 + bhead] * ccol;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) s2[tile][r] = __builtin_fmaf(d[r], crow[r], bc);
+            for (int r = 0; r < 4; ++r) s2[tile][r] = __builtin_fmaf(d[r] + dpp<0x128>(d[r]), crow[r], bc);
         }
 
+        const bool full = (vmask == 0xffffffffu);
         if (!full) {
 #pragma unroll
             for (int tile = 0; tile < 2; ++tile)
@@ -367,14 +590,19 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
                     if (!((vmask >> (16 * tile + 4 * gk + r)) & 1u)) s2[tile][r] = kNegInf;
         }
         if (a.logits && n < gc) {
-            float* row = a.logits + static_cast<size_t>(kvh * G + g0 + n) * a.ld + Nd + 32 * p;
+            float* row = a.logits + static_cast<size_t>(kvh * G + g0 + n) * a.ld + Nd + 32 * p + 4 * gk;
+            if (32 * p + 32 <= nslots) {
 #pragma unroll
-            for (int tile = 0; tile < 2; ++tile)
+                for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int t = 16 * tile + 4 * gk + r;
-                    if (32 * p + t < nslots) row[t] = s2[tile][r];
-                }
+                    for (int r = 0; r < 4; ++r) row[16 * tile + r] = s2[tile][r];
+            } else {
+#pragma unroll
+                for (int tile = 0; tile < 2; ++tile)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (32 * p + 16 * tile + 4 * gk + r < nslots) row[16 * tile + r] = s2[tile][r];
+            }
         }
 
         // V scale / zero of this lane's tokens: [tile 0 r 0..3, tile 1 r 0..3].
@@ -385,25 +613,18 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         const float vsv[2][4] = {{va.x, va.y, va.z, va.w}, {vb.x, vb.y, vb.z, vb.w}};
         const float vzv[2][4] = {{za.x, za.y, za.z, za.w}, {zb.x, zb.y, zb.z, zb.w}};
 
-        float mx = kNegInf, vmx = 0.0f;
-#pragma unroll
-        for (int tile = 0; tile < 2; ++tile)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                mx = fmaxf(mx, s2[tile][r]);
-                const float av = fabsf(vsv[tile][r]);
-                vmx = fmaxf(vmx, (full || s2[tile][r] != kNegInf) ? av : 0.0f);
-            }
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
-        vmx = fmaxf(vmx, shfl_xor(vmx, 16));
-        vmx = fmaxf(vmx, shfl_xor(vmx, 32));
+        float mx = fmaxf(fmaxf(fmaxf(s2[0][0], s2[0][1]), fmaxf(s2[0][2], s2[0][3])),
+                         fmaxf(fmaxf(s2[1][0], s2[1][1]), fmaxf(s2[1][2], s2[1][3])));
+        float vmx = fmaxf(fmaxf(fmaxf(fabsf(va.x), fabsf(va.y)), fmaxf(fabsf(va.z), fabsf(va.w))),
+                          fmaxf(fmaxf(fabsf(vb.x), fabsf(vb.y)), fmaxf(fabsf(vb.z), fabsf(vb.w))));
+        mx = xrow_max(mx);
+        vmx = xrow_max(vmx);
         const int ev = (vmx > 0.0f) ? __builtin_amdgcn_frexp_expf(vmx) : 0;
         const float cand = mx - static_cast<float>(13 - ev);
         const bool up = cand > m_run + kMfTau;
         if (__ballot(up)) {
             const float mn = up ? cand : m_run;
-            const float al = up ? exp2f(m_run - mn) : 1.0f;
+            const float al = up ? __builtin_amdgcn_exp2f(m_run - mn) : 1.0f;
             l_run *= al;
             pz *= al;
 #pragma unroll
@@ -421,17 +642,15 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         for (int tile = 0; tile < 2; ++tile)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                float e = exp2f(s2[tile][r] - m_run);
-                if (!full) e = (s2[tile][r] == kNegInf) ? 0.0f : e;
+                const float e = __builtin_amdgcn_exp2f(s2[tile][r] - m_run);  // flushes below 2^-126
                 lsum += e;
-                // invalid slots may hold any scale / zero: keep them out of the sums
-                const bool use = full || e != 0.0f;
-                pz = use ? __builtin_fmaf(e, vzv[tile][r], pz) : pz;
-                pv[tile][r] = use ? e * vsv[tile][r] : 0.0f;
+                pz = __builtin_fmaf(e, vzv[tile][r], pz);
+                pv[tile][r] = e * vsv[tile][r];
             }
         l_run += lsum;
         mf_u4 ahi, alo;
         split_hl4(pv[0][0], pv[0][2], pv[0][1], pv[0][3], pv[1][0], pv[1][2], pv[1][1], pv[1][3], ahi, alo);
+        const mf_u4 ap = lo_col ? alo : ahi;
 
         // B: codes of channel 4 beta + k for the lane's 8 tokens,
         // beta = n (nsteps 0..3) and n + 16 (nsteps 4..7), k = nstep & 3.
@@ -442,20 +661,23 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const uint32_t mk = (3u << (2 * k)) | (3u << (16 + 2 * k));
-            const mf_u4 b0 = {code_f16(q0.x, mk), code_f16(q0a, mk), code_f16(q0.y, mk), code_f16(q0b, mk)};
-            acc[k] = mfma16x16x32(ahi, b0, acc[k]);
-            acc[k] = mfma16x16x32(alo, b0, acc[k]);
-            const mf_u4 b1 = {code_f16(q1.x, mk), code_f16(q1a, mk), code_f16(q1.y, mk), code_f16(q1b, mk)};
-            acc[4 + k] = mfma16x16x32(ahi, b1, acc[4 + k]);
-            acc[4 + k] = mfma16x16x32(alo, b1, acc[4 + k]);
+            const mf_u4 b0 = {code_f16(q0.x, mk, one024), code_f16(q0a, mk, one024), code_f16(q0.y, mk, one024),
+                              code_f16(q0b, mk, one024)};
+            acc[k] = mfma16x16x32(ap, b0, acc[k]);
+            const mf_u4 b1 = {code_f16(q1.x, mk, one024), code_f16(q1a, mk, one024), code_f16(q1.y, mk, one024),
+                              code_f16(q1b, mk, one024)};
+            acc[4 + k] = mfma16x16x32(ap, b1, acc[4 + k]);
         }
         wave_lds_sync();
     }
 
-    l_run += shfl_xor(l_run, 16);
-    l_run += shfl_xor(l_run, 32);
-    pz += shfl_xor(pz, 16);
-    pz += shfl_xor(pz, 32);
+    l_run = xrow_sum(l_run);
+    pz = xrow_sum(pz);
+    // rows h + 8 (low parts, lanes 32..63) onto rows h (lanes 0..31)
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[s][r] = xhalf_sum(acc[s][r]);
 
     __syncthreads();  // every wave is done with its staging area
     float* sm_m = reinterpret_cast<float*>(lds);  // [4][GP]
@@ -467,36 +689,39 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         sm_l[wave * GP + lane] = l_run;
         sm_z[wave * GP + lane] = pz;
     }
+    if (lane < 32) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s)
+        for (int s = 0; s < 8; ++s)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int h = 4 * gk + r;
-            if (h < GP) {
-                const int c = 4 * n + 64 * (s >> 2) + (s & 3);
-                sm_acc[(wave * GP + h) * kMfD + c] = __builtin_amdgcn_ldexpf(acc[s][r], -2 * (s & 3));
+            for (int r = 0; r < 4; ++r) {
+                const int h = 4 * gk + r;
+                if (h < GP) {
+                    const int c = 4 * n + 64 * (s >> 2) + (s & 3);
+                    sm_acc[(wave * GP + h) * kMfD + c] = __builtin_amdgcn_ldexpf(acc[s][r], -2 * (s & 3));
+                }
             }
-        }
+    }
     __syncthreads();
     for (int idx = threadIdx.x; idx < gc * kMfD; idx += 256) {
         const int g = idx / kMfD, c = idx - g * kMfD;
-        float M = kNegInf;
+        float M = -1.0e30f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w * GP + g]);
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, fmaxf(sm_m[w * GP + g], dl[(w * GP + g) * (2 + kMfD)]));
         float A = 0.0f, Ls = 0.0f;
-        if (M != kNegInf) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const float mw = sm_m[w * GP + g];
-                const float f = (mw == kNegInf) ? 0.0f : exp2f(mw - M);
-                A = __builtin_fmaf(f, sm_acc[(w * GP + g) * kMfD + c] + sm_z[w * GP + g], A);
-                Ls = __builtin_fmaf(f, sm_l[w * GP + g], Ls);
-            }
+        for (int w = 0; w < 4; ++w) {
+            const float f = exp2f(sm_m[w * GP + g] - M);
+            A = __builtin_fmaf(f, sm_acc[(w * GP + g) * kMfD + c] + sm_z[w * GP + g], A);
+            Ls = __builtin_fmaf(f, sm_l[w * GP + g], Ls);
+            const float* dg = dl + (w * GP + g) * (2 + kMfD);
+            const float fd = (dg[0] == kNegInf) ? 0.0f : exp2f(dg[0] - M);
+            A = __builtin_fmaf(fd, dg[2 + c], A);
+            Ls = __builtin_fmaf(fd, dg[1], Ls);
         }
         const size_t pi = static_cast<size_t>(kvh * G + g0 + g) * a.nsplit + split;
         a.part_acc[pi * kMfD + c] = A;
         if (c == 0) {
-            a.part_ml[2 * pi] = M;
+            a.part_ml[2 * pi] = (Ls > 0.0f) ? M : kNegInf;
             a.part_ml[2 * pi + 1] = Ls;
         }
     }
