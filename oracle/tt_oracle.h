@@ -11,7 +11,7 @@
  * performs is written as an explicit fmaf). Citations are to the reference
  * repository (RahulGPi/TriTierCache).
  *
- * Parity pins (how each function is checked, see tests/test_oracle_*.py):
+ * Parity pins (how each function is checked, see tests/test_oracle.py):
  *   orc_quantize_v_block   reference KAT vectors (tests/test_quantize_v.cpp,
  *                          tests/tie_test_v.cpp) + bit-exact vs compiled reference
  *   orc_quantize_k_block   bit-exact vs compiled reference + closed-form brute force

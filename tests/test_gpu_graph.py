@@ -1,0 +1,122 @@
+"""HIP-graph capture and replay of the stateless entry points (through the C ABI).
+
+Each captured call is replayed several times with new inputs written into the
+captured buffers between replays (eager kernels of the program itself run in
+between), and every replay must match an eager call on the same inputs bit for
+bit: the kernels are deterministic (no atomics, fixed merge order), and any
+memset node or stale argument recorded in the graph would show up here.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import synth
+from gpu_helpers import dev, host, rel_err, same_bits
+import test_gpu_kernels as K
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def lib():
+    assert torch.cuda.is_available(), "GPU test on a machine without a GPU"
+    from tritiercache_amd import _lib
+
+    return _lib
+
+
+def _stream():
+    return C.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,nd,nb,kgs,fp16,mask", [
+    (32, 8, 128, 70, 40, 16, False, "holes"),
+    (28, 4, 128, 33, 21, 16, True, "tail"),
+    (8, 2, 64, 17, 9, 32, False, "none"),
+])
+def test_fused_attention_graph_replays(lib, oracle, Hq, Hkv, D, nd, nb, kgs, fp16, mask):
+    L = lib.load()
+    args = K.make_case(oracle, Hq, Hkv, D, nd, nb, kgs, fp16, mask, seed=900 + Hq)
+    (Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, fp16) = args
+    t = {k: dev(v) for k, v in dict(Q=Q, dK=dK, dV=dV, KP=KP, KS=KS, KZ=KZ, VP=VP, VS=VS, VZ=VZ, ids=ids).items()}
+    n = nd + nb * kgs
+    ws_bytes = int(L.tt_fused_attention_workspace_bytes(nd, nb, Hq, Hkv, D, kgs, 1))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+
+    def call(out, mw, work):
+        rc = L.tt_fused_attention_decode_ws(
+            t["Q"].data_ptr(), t["dK"].data_ptr(), t["dV"].data_ptr(), nd, t["KP"].data_ptr(), t["KS"].data_ptr(),
+            t["KZ"].data_ptr(), t["VP"].data_ptr(), t["VS"].data_ptr(), t["VZ"].data_ptr(), t["ids"].data_ptr(), nb,
+            Hq, Hkv, D, out.data_ptr(), mw.data_ptr(), kgs, int(fp16), work.data_ptr(), ws_bytes, _stream())
+        lib.check(rc, "fused_attention_decode_ws")
+
+    g_out = torch.zeros((Hq, D), device="cuda")
+    g_mw = torch.zeros((n,), device="cuda")
+    call(g_out, g_mw, ws)  # warm-up outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(g_out, g_mw, ws)
+
+    e_out = torch.zeros_like(g_out)
+    e_mw = torch.zeros_like(g_mw)
+    e_ws = torch.empty_like(ws)
+    for rep in range(4):
+        # new query (and new dense keys on odd replays) in the captured buffers
+        t["Q"].copy_(dev(synth.normal(7000 + rep, 0, (Hq, D))))
+        if rep % 2:
+            t["dK"].mul_(-0.5)
+        g_out.fill_(float("nan"))
+        g_mw.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        call(e_out, e_mw, e_ws)
+        torch.cuda.synchronize()
+        assert torch.equal(g_out, e_out), rep
+        assert torch.equal(g_mw, e_mw), rep
+        # and the replay is right, not only repeatable
+        hargs = (host(t["Q"]), host(t["dK"]), dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, fp16)
+        ro, rmw = oracle.fused_attention_decode(*hargs)
+        assert rel_err(host(g_out), ro) <= K.ATTN_TOL, rep
+        assert rel_err(host(g_mw), rmw) <= K.ATTN_TOL, rep
+
+
+def test_quantizers_graph_replays(lib, oracle):
+    L = lib.load()
+    kgs, H, D, nblk = 16, 8, 128, 6
+    Kt = torch.zeros((nblk * kgs, H, D), device="cuda")
+    Vt = torch.zeros((nblk * kgs, H, D), device="cuda")
+    kp = torch.zeros((nblk, H, D), dtype=torch.int32, device="cuda")
+    ks = torch.zeros((nblk, H, D), device="cuda")
+    kz = torch.zeros((nblk, H, D), device="cuda")
+    vp = torch.zeros((nblk * kgs, H, D // 16), dtype=torch.int32, device="cuda")
+    vs = torch.zeros((nblk * kgs, H), device="cuda")
+    vz = torch.zeros((nblk * kgs, H), device="cuda")
+
+    def call():
+        lib.check(L.tt_quantize_k_block(Kt.data_ptr(), kp.data_ptr(), ks.data_ptr(), kz.data_ptr(), nblk, H, D, kgs,
+                                        0, _stream()), "quantize_k")
+        lib.check(L.tt_quantize_v_block(Vt.data_ptr(), vp.data_ptr(), vs.data_ptr(), vz.data_ptr(), nblk * kgs, H, D,
+                                        0, _stream()), "quantize_v")
+
+    call()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for rep in range(3):
+        Kh = synth.normal(8100 + rep, 0, (nblk * kgs, H, D)) * np.float32(1 + rep)
+        Vh = synth.normal(8100 + rep, 1, (nblk * kgs, H, D))
+        Kt.copy_(dev(Kh))
+        Vt.copy_(dev(Vh))
+        kp.fill_(-1)
+        vp.fill_(-1)
+        g.replay()
+        torch.cuda.synchronize()
+        for b in range(nblk):
+            p, s, z = oracle.quantize_k(Kh[b * kgs:(b + 1) * kgs], kgs, False)
+            assert same_bits(host(kp[b:b + 1]), p) and same_bits(host(ks[b]), s) and same_bits(host(kz[b]), z), rep
+        p, s, z = oracle.quantize_v(Vh, False)
+        assert same_bits(host(vp), p) and same_bits(host(vs), s) and same_bits(host(vz), z), rep
