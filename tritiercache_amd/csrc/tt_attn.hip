@@ -390,12 +390,19 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
 
 #include "tt_attn_mfma.h"
 
-// head_dim 128: the matrix-core loop over the packed store, each workgroup
-// with a share of the FP32 tiles as a VALU prologue (grid nsplit_p x Hkv x
-// head chunks).
+// head_dim 128: grid (nsplit_p + nsplit_d) x Hkv x head chunks. Workgroups
+// x < nsplit_p run the matrix-core loop over the packed store, the others a
+// VALU pass over a share of the FP32 tiers; every workgroup writes its own
+// partial slot.
 template <int GP, typename MetaT>
 __global__ void __launch_bounds__(256) attn_packed_kernel(SplitArgs a) {
-    __shared__ __align__(16) char lds[MfLds<GP>::TOTAL];
+    constexpr int kLds = MfLds<GP>::TOTAL > DnLds<GP>::TOTAL ? MfLds<GP>::TOTAL : DnLds<GP>::TOTAL;
+    __shared__ __align__(16) char lds[kLds];
+    const int bx = static_cast<int>(blockIdx.x);
+    if (bx >= a.nsplit_p) {
+        dense_body<GP>(a, bx - a.nsplit_p, lds);
+        return;
+    }
     // The KV heads of one tile sit side by side in memory (512-byte K rows,
     // 32-byte V rows): rotate each head's split index so the workgroups that
     // run together stream different regions instead of the same DRAM pages.
@@ -403,7 +410,7 @@ __global__ void __launch_bounds__(256) attn_packed_kernel(SplitArgs a) {
     const int hid = static_cast<int>(blockIdx.y * gridDim.z + blockIdx.z);
     const int rot = static_cast<int>(static_cast<unsigned>(a.nsplit_p) * static_cast<unsigned>(hid) /
                                      static_cast<unsigned>(heads));
-    int split = static_cast<int>(blockIdx.x) + rot;
+    int split = bx + rot;
     split = split >= a.nsplit_p ? split - a.nsplit_p : split;
     packed_body<GP, MetaT>(a, __builtin_amdgcn_readfirstlane(split), lds);
 }
@@ -413,7 +420,7 @@ __global__ void __launch_bounds__(256) attn_packed_kernel(SplitArgs a) {
 //   [0, Hq)        merge the split partials of query head h (log2 units):
 //                  M = max_j m_j, L = sum_j l_j 2^(m_j - M),
 //                  out = sum_j acc_j 2^(m_j - M) / L.
-//   [Hq, ...)      mean attention weights of 256 tokens each
+//   [Hq, ...)      mean attention weights of kMeanTokens tokens each
 //                  (fused_attn_avx2.cpp:286-300): every such workgroup first
 //                  rebuilds (M, 1/L) of all heads from the (m, l) partials,
 //                  then w_h = 2^(s_h - M_h) / L_h summed over the heads and
@@ -461,7 +468,9 @@ __device__ __forceinline__ float wave_sum(float x) {
 
 // Merge of query head h. Every load is issued before the first reduction:
 // thread t holds (m_t, l_t) of split t, and thread (group g, channel quad c4)
-// the accumulators of splits g, g + groups, ... (unrolled in batches of 8).
+// the accumulators of splits g, g + groups, ... (up to kMergeU per group and
+// block of 256 splits, all in flight together).
+constexpr int kMergeU = 16;
 __device__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
@@ -478,10 +487,10 @@ __device__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
         const int jt = j0 + t;
         const float mt = jt < a.nsplit ? ml[2 * jt] : kNegInf;
         const float lt = jt < a.nsplit ? ml[2 * jt + 1] : 0.0f;
-        float4 v[8];
-        float mv[8];
+        float4 v[kMergeU];
+        float mv[kMergeU];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kMergeU; ++u) {
             const int j = j0 + g + u * groups;
             const bool in = g < groups && j < a.nsplit && j < j0 + 256;
             v[u] = in ? *reinterpret_cast<const float4*>(base + static_cast<size_t>(j) * a.D)
@@ -499,15 +508,15 @@ __device__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
         const float al = (M == kNegInf) ? 0.0f : exp2f(M - Mn);
         A.x *= al; A.y *= al; A.z *= al; A.w *= al;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < kMergeU; ++u) {
             const float f = (mv[u] == kNegInf) ? 0.0f : exp2f(mv[u] - Mn);
             A.x = __builtin_fmaf(f, v[u].x, A.x);
             A.y = __builtin_fmaf(f, v[u].y, A.y);
             A.z = __builtin_fmaf(f, v[u].z, A.z);
             A.w = __builtin_fmaf(f, v[u].w, A.w);
         }
-        // splits beyond 8 per group in this block of 256 (only when groups < 32)
-        for (int j = j0 + g + 8 * groups; g < groups && j < a.nsplit && j < j0 + 256; j += groups) {
+        // splits beyond kMergeU per group in this block of 256 (groups < 16 only)
+        for (int j = j0 + g + kMergeU * groups; g < groups && j < a.nsplit && j < j0 + 256; j += groups) {
             const float mj = ml[2 * j];
             const float f = (mj == kNegInf) ? 0.0f : exp2f(mj - Mn);
             const float4 w = *reinterpret_cast<const float4*>(base + static_cast<size_t>(j) * a.D);
@@ -547,6 +556,13 @@ __device__ __forceinline__ float sum8(float x) {
     return x + dpp<0x141>(x);
 }
 
+#ifndef TT_MEAN_TOKENS
+#define TT_MEAN_TOKENS 64
+#endif
+constexpr int kMeanTokens = TT_MEAN_TOKENS;  // tokens per mean-weight workgroup
+constexpr int kMeanQuads = kMeanTokens / 4;  // token quads per workgroup
+constexpr int kMeanGroups = 256 / kMeanQuads;  // head groups per workgroup
+
 __device__ void fin_mean_tokens(const FinArgs& a, const int blk, float* sh) {
     const int t = threadIdx.x;
     const int Hq = a.Hq;
@@ -560,18 +576,19 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int blk, float* sh) {
         Nd = s + hh + rw;
         n = Nd + a.state[kBlocksUsed] * a.kgs;
     }
-    const int tok0 = blk * 256;
+    const int tok0 = blk * kMeanTokens;
     if (tok0 >= n) return;
-    // Thread (head group hg, token quad q): heads hg, hg + 4, ...; tokens
-    // tok0 + 4 q .. + 3. Rows are padded to a multiple of 4 floats. The
-    // logits of the first 32 heads are loaded before anything else.
-    const int q = t & 63, hg = t >> 6;
+    // Thread (head group hg, token quad q): heads hg, hg + kMeanGroups, ...;
+    // tokens tok0 + 4 q .. + 3. Rows are padded to a multiple of 4 floats.
+    // The logits of the first 8 kMeanGroups heads are loaded before anything
+    // else.
+    const int q = t % kMeanQuads, hg = t / kMeanQuads;
     const int i0 = tok0 + 4 * q;
     const bool whole = i0 + 4 <= n;
     float4 lgv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-        const int h = hg + 4 * u;
+        const int h = hg + kMeanGroups * u;
         lgv[u] = make_float4(kNegInf, kNegInf, kNegInf, kNegInf);
         if (h < Hq && i0 < n) {
             const float* lg = a.logits + static_cast<size_t>(h) * a.ld + i0;
@@ -591,21 +608,21 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int blk, float* sh) {
         const int h = h0 + (t >> 3), j0 = t & 7;
         const float* ml = a.part_ml + static_cast<size_t>(h < Hq ? h : 0) * a.nsplit * 2;
         float mx = kNegInf, ls = 0.0f;
-        for (int jb = j0; jb < a.nsplit; jb += 64) {
-            float mv[8], lv[8];
+        for (int jb = j0; jb < a.nsplit; jb += 8 * kMergeU) {
+            float mv[kMergeU], lv[kMergeU];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
+            for (int u = 0; u < kMergeU; ++u) {
                 const int j = jb + 8 * u;
                 mv[u] = j < a.nsplit ? ml[2 * j] : kNegInf;
                 lv[u] = j < a.nsplit ? ml[2 * j + 1] : 0.0f;
             }
             float bm = kNegInf;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) bm = fmaxf(bm, mv[u]);
+            for (int u = 0; u < kMergeU; ++u) bm = fmaxf(bm, mv[u]);
             const float mn = fmaxf(mx, bm);
             float bs = 0.0f;
 #pragma unroll
-            for (int u = 0; u < 8; ++u) bs += (mv[u] == kNegInf) ? 0.0f : exp2f(mv[u] - mn) * lv[u];
+            for (int u = 0; u < kMergeU; ++u) bs += (mv[u] == kNegInf) ? 0.0f : exp2f(mv[u] - mn) * lv[u];
             ls = ((mx == kNegInf) ? 0.0f : ls * exp2f(mx - mn)) + bs;
             mx = mn;
         }
@@ -619,10 +636,10 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int blk, float* sh) {
     __syncthreads();
     float w4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
     if (i0 < n) {
-        for (int hb = 0; hb < Hq; hb += 32) {
+        for (int hb = 0; hb < Hq; hb += 8 * kMeanGroups) {
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                const int h = hb + hg + 4 * u;
+                const int h = hb + hg + kMeanGroups * u;
                 if (h >= Hq) break;
                 float4 v;
                 if (hb == 0) {
@@ -642,7 +659,8 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int blk, float* sh) {
                 const float mh = Mh[h], il = iL[h];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const float w = (sc[e] == kNegInf) ? 0.0f : exp2f(sc[e] - mh) * il;
+                    // s <= M_h, so 2^(s - M_h) <= 1 (flushed to 0 below 2^-126)
+                    const float w = (sc[e] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(sc[e] - mh) * il;
                     w4[e] += w;
                     if (a.head_w && i0 + e < n && i0 + e < a.head_w_ld)
                         a.head_w[static_cast<size_t>(h) * a.head_w_ld + i0 + e] = w;
@@ -650,13 +668,16 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int blk, float* sh) {
             }
         }
     }
-    float* red = sh + 2 * Hq;  // [4][256]
+    float* red = sh + 2 * Hq;  // [kMeanGroups][kMeanTokens]
 #pragma unroll
-    for (int e = 0; e < 4; ++e) red[hg * 256 + 4 * q + e] = w4[e];
+    for (int e = 0; e < 4; ++e) red[hg * kMeanTokens + 4 * q + e] = w4[e];
     __syncthreads();
+    if (t >= kMeanTokens) return;
     const int i = tok0 + t;
     if (i >= n) return;
-    const float sum = (red[t] + red[256 + t]) + (red[512 + t] + red[768 + t]);
+    float sum = 0.0f;
+#pragma unroll
+    for (int g = 0; g < kMeanGroups; ++g) sum += red[g * kMeanTokens + t];
     const float mean = sum / static_cast<float>(Hq);
     if (a.mw) a.mw[i] = mean;
     if (a.fb.g) {
@@ -816,12 +837,22 @@ AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs,
     const long long per_head = std::max<long long>(1, (resident + heads - 1) / heads);
     const long long dense_tiles = (dense_ub + 15) / 16;
     if (use_packed_kernel(D)) {
-        // One resident round of workgroups, each with at least ~8 pairs of
-        // packed tiles (or 2 FP32 tiles) so the partials stay small.
+        // One resident round of workgroups per head, at least ~8 units of work
+        // each so the partials stay small (a 32-token pair of packed tiles is
+        // one unit, a 16-token FP32 tile kDenseTileCost), shared between packed
+        // and FP32 workgroups in proportion to their work.
+        constexpr long long kDenseTileCost = 2;
         const long long pairs = (static_cast<long long>(blocks_ub) * W + 1) / 2;
-        const long long work = std::max(pairs / 8, dense_tiles / 2);
-        p.nsplit_d = 0;
-        p.nsplit_p = static_cast<int>(std::max<long long>(1, std::min(per_head, work)));
+        const long long dense_units = dense_tiles * kDenseTileCost;
+        const long long units = pairs + dense_units;
+        const long long wgs = std::max<long long>(1, std::min(per_head, units / 8));
+        long long nd = 0;
+        if (dense_tiles > 0) {
+            nd = (wgs * dense_units + units / 2) / units;
+            nd = std::max<long long>(1, std::min(nd, dense_tiles));
+        }
+        p.nsplit_d = static_cast<int>(nd);
+        p.nsplit_p = static_cast<int>(std::max<long long>(1, wgs - nd));
     } else {
         // One round of resident workgroups, but at least ~32 packed-tile
         // units of work per workgroup so the merge traffic stays small.
@@ -865,8 +896,8 @@ int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipS
     const int gp = gp_for(G);
     const int chunks = (G + gp - 1) / gp;
     if (use_packed_kernel(in.D)) {
-        if (plan.nsplit_p <= 0 || plan.nsplit_d != 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
-        return launch_packed(a, dim3(plan.nsplit_p, in.Hkv, chunks), gp, in.meta_fp16, stream);
+        if (plan.nsplit_p <= 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
+        return launch_packed(a, dim3(plan.nsplit, in.Hkv, chunks), gp, in.meta_fp16, stream);
     }
     const dim3 grid(plan.nsplit, in.Hkv, chunks);
     if (plan.nsplit_p != 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
@@ -900,8 +931,8 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
     f.head_w = head_w;
     f.head_w_ld = head_w_ld;
     f.fb = fb ? *fb : Feedback{};
-    const int mean_wgs = weights ? (std::max(plan.token_ub, 1) + 255) / 256 : 0;
-    const size_t lds = sizeof(float) * std::max<size_t>(8 + 4 * 256, 2 * static_cast<size_t>(in.Hq) + 4 * 256);
+    const int mean_wgs = weights ? (std::max(plan.token_ub, 1) + kMeanTokens - 1) / kMeanTokens : 0;
+    const size_t lds = sizeof(float) * std::max<size_t>(8 + 4 * 256, 2 * static_cast<size_t>(in.Hq) + 256 * 4);
     hipLaunchKernelGGL(attn_finalize_kernel, dim3(in.Hq + mean_wgs), dim3(256), lds, stream, f);
     TT_LAUNCH_CHECK();
     return TT_OK;

@@ -48,24 +48,39 @@ typedef uint32_t mf_u4 __attribute__((ext_vector_type(4)));
 constexpr int kMfD = 128;       // head_dim of this path
 constexpr float kMfTau = 2.0f;  // slack of the lazy rescale, log2 units
 
-// Per-wave LDS staging of one 32-token pair (byte offsets).
+// Per-wave LDS staging of one 32-token pair (byte offsets). Row strides are
+// padded so that the wide LDS accesses of one instruction (8 lanes x 16
+// bytes, 16 lanes x 8 bytes) fall into distinct banks.
+constexpr int kKTS = 36;   // dwords per K row (token quad): 128 channel bytes + 4 dwords pad
+constexpr int kVTS = 10;   // dwords per V byte column: 32 token bytes + 2 dwords pad
+constexpr int kKSZ = 144;  // floats per K scale (zero) row: channel c at c + 4 (c / 32)
+constexpr int kBRS = 136;  // halves per coefficient row: 128 + 8 pad
 template <int GP>
 struct MfLds {
-    static constexpr int KT = 0;       // [2 tiles][4 token quads][128 channel bytes]
-    static constexpr int VT = 1024;    // [32 byte columns][32 token bytes in MFMA order]
-    static constexpr int KSZ = 2048;   // [2 tiles][scale | zero][128] f32
-    static constexpr int VS = 4096;    // [32] f32, MFMA token order (0 for masked slots)
-    static constexpr int VZ = 4224;    // [32] f32
-    static constexpr int BIAS = 4352;  // [2 tiles][8] f32 per-head QK bias
-    static constexpr int BHL = 4416;   // [2 tiles][hi rows 0..GP-1, lo rows GP..2GP-1][128] f16
-    static constexpr int BHL_TILE = 2 * GP * kMfD * 2;
+    static constexpr int KT = 0;       // [2 tiles][4 token quads][kKTS dwords]
+    static constexpr int VT = 1152;    // [32 byte columns][kVTS dwords], token bytes in MFMA order
+    static constexpr int KSZ = 2432;   // [2 tiles][scale | zero][kKSZ] f32
+    static constexpr int VS = 4736;    // [32] f32, MFMA token order (0 for masked slots)
+    static constexpr int VZ = 4864;    // [32] f32
+    static constexpr int BIAS = 4992;  // [2 tiles][8] f32 per-head QK bias
+    static constexpr int BHL = 5056;   // [2 tiles][hi rows 0..GP-1, lo rows GP..2GP-1][kBRS] f16
+    static constexpr int BHL_TILE = 2 * GP * kBRS * 2;
     static constexpr int BYTES = BHL + 2 * BHL_TILE;
     // final merge of the four waves, reusing the staging area
     static constexpr int MERGE = 4 * GP * (3 + kMfD) * 4;
     static_assert(MERGE <= 4 * BYTES, "merge area must fit in the staging area");
-    // per-wave dense partials [4][GP][max, sum, acc[128]], after the four staging areas
-    static constexpr int DENSE = 4 * BYTES;
-    static constexpr int TOTAL = DENSE + 4 * GP * (2 + kMfD) * 4;
+    // the workgroup's query heads [GP][128] f32, after the four staging areas
+    static constexpr int QL = 4 * BYTES;
+    static constexpr int TOTAL = QL + GP * kMfD * 4;
+};
+
+// LDS of an FP32-tier workgroup (byte offsets): the query heads, then the
+// per-wave partials [4][GP][max, sum, acc[128]].
+template <int GP>
+struct DnLds {
+    static constexpr int QL = 0;
+    static constexpr int PART = GP * kMfD * 4;
+    static constexpr int TOTAL = PART + 4 * GP * (2 + kMfD) * 4;
 };
 
 // Reductions over the four 16-lane rows of a wave (lanes n, n+16, n+32, n+48).
@@ -167,56 +182,97 @@ __device__ __forceinline__ int part_begin(const int count, const int i, const in
         static_cast<int>(static_cast<unsigned>(count) * static_cast<unsigned>(i) / static_cast<unsigned>(parts)));
 }
 
-// FP32 16-token tiles of workgroup `split` (its share of the dense tiers).
-__device__ __forceinline__ void dense_range(const SplitArgs& a, const int split, int& d0, int& d1) {
-    const AttnInputs& in = a.in;
-    int Nd = in.n0 + in.n1 + in.n2;
-    if (in.state) Nd = in.state[kSCount] + in.state[kHhCount] + in.state[kRwCount];
+// FP32 16-token tiles [d0, d1) of FP32 workgroup `dsplit` of nsplit_d.
+__device__ __forceinline__ void dense_range(const SplitArgs& a, const int Nd, const int dsplit, int& d0, int& d1) {
     const int Td = (Nd + 15) >> 4;
-    d0 = part_begin(Td, split, a.nsplit_p);
-    d1 = part_begin(Td, split + 1, a.nsplit_p);
+    d0 = part_begin(Td, dsplit, a.nsplit_d);
+    d1 = part_begin(Td, dsplit + 1, a.nsplit_d);
 }
 
-// FP32 tiers of the workgroup's share (16-token tiles [d0, d1) of the logical
-// dense order sinks -> heavy hitters -> recent ring), VALU, before the packed
-// loop. Wave w takes tiles d0 + w, d0 + w + 4, ...; lanes are (token group tg
-// = lane / 16) x (8-channel slice cp = lane % 16), the query heads of the
-// group in passes of up to four. Leaves one (max, sum, acc[128]) partial per
-// head in `dl` ([GP][2 + 128] per wave) and writes the dense logits.
+// The group's query heads into LDS ([GP][128] f32, heads past gc as zeros).
+// Issued before any other global load of the workgroup: loads return in
+// order, so the barrier that follows then waits for this load only.
 template <int GP>
-__device__ __forceinline__ void dense_share(const SplitArgs& a, const int split, const int kvh, const int g0,
-                                            const int gc, const int wave, float* dl) {
+__device__ __forceinline__ void load_q_lds(const AttnInputs& in, const int kvh, const int g0, const int gc,
+                                           float* q_l) {
+    const int G = in.Hq / in.Hkv;
+    for (int idx = threadIdx.x; idx < GP * (kMfD / 4); idx += 256) {
+        const int g = idx / (kMfD / 4), c4 = idx - g * (kMfD / 4);
+        float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (g < gc) v = *reinterpret_cast<const float4*>(in.Q + static_cast<size_t>(kvh * G + g0 + g) * kMfD + 4 * c4);
+        *reinterpret_cast<float4*>(q_l + g * kMfD + 4 * c4) = v;
+    }
+}
+
+// Tier pointers and counts of the FP32 tokens (device counters for the engine).
+struct DenseView {
+    int n0, n1, n2, head, Nd;
+};
+
+__device__ __forceinline__ DenseView dense_view(const AttnInputs& in) {
+    DenseView v{in.n0, in.n1, in.n2, in.ring_head, 0};
+    if (in.state) {
+        v.n0 = in.state[kSCount];
+        v.n1 = in.state[kHhCount];
+        v.n2 = in.state[kRwCount];
+        v.head = in.state[kRwHead];
+    }
+    v.Nd = v.n0 + v.n1 + v.n2;
+    return v;
+}
+
+// Keys and values of one 16-token FP32 tile for one lane: the four tokens of
+// token group tg = lane / 16, channels 8 cp .. 8 cp + 7 (cp = lane % 16).
+struct DenseTile {
+    float kx[4][8], vx[4][8];
+};
+
+// Issues the loads of tile k (logical order sinks -> heavy hitters -> recent
+// ring). Rows past the tiers repeat the last row (finite data, masked later).
+__device__ __forceinline__ void dense_load(const AttnInputs& in, const DenseView& dv, const int kvh, const int k,
+                                           DenseTile& t) {
+    const int lane = threadIdx.x & 63;
+    const int tg = lane >> 4, cp = lane & 15;
+    const int tok0 = 16 * k + 4 * tg;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r0 = tok0 + i;
+        const int r = r0 < dv.Nd ? r0 : dv.Nd - 1;
+        const bool in0 = r < dv.n0, in1 = r < dv.n0 + dv.n1;
+        int ring = dv.head + (r - dv.n0 - dv.n1);
+        ring = ring >= in.ring_size ? ring - in.ring_size : ring;
+        const int idx = in0 ? r : (in1 ? r - dv.n0 : ring);
+        const float* kb = in0 ? in.k0 : (in1 ? in.k1 : in.k2);
+        const float* vb = in0 ? in.v0 : (in1 ? in.v1 : in.v2);
+        const int off = (idx * in.Hkv + kvh) * kMfD + cp * 8;
+        load_f32<8>(kb + off, t.kx[i]);
+        load_f32<8>(vb + off, t.vx[i]);
+    }
+}
+
+// FP32 tiers of the workgroup's share (16-token tiles [d0, d1)), VALU.
+// Wave w takes tiles d0 + w, d0 + w + 4, ...; the caller has
+// already issued the loads of the first one into `t0`, the others are loaded
+// as they come (a wave rarely has more than one). Lanes are (token group
+// tg = lane / 16) x (8-channel slice cp = lane % 16), the query heads of the
+// group in passes of up to four, read from the workgroup's copy of Q in LDS
+// (`q_l`, [GP][128]). Leaves one (max, sum, acc[128]) partial per head in `dl`
+// ([GP][2 + 128] per wave) and writes the dense logits.
+template <int GP>
+__device__ __forceinline__ void dense_share(const SplitArgs& a, const DenseView& dv, const int d0, const int d1,
+                                            const int kvh, const int g0, const int gc, const int wave,
+                                            const float* q_l, const DenseTile& t0, float* dl) {
     constexpr int HP = GP < 4 ? GP : 4;
     constexpr int NPASS = GP / HP;
     const AttnInputs& in = a.in;
     const int lane = threadIdx.x & 63;
     const int tg = lane >> 4, cp = lane & 15;
     const int G = in.Hq / in.Hkv;
-    const int Hkv = in.Hkv;
-    int n0 = in.n0, n1 = in.n1, n2 = in.n2, head = in.ring_head;
-    if (in.state) {
-        n0 = in.state[kSCount];
-        n1 = in.state[kHhCount];
-        n2 = in.state[kRwCount];
-        head = in.state[kRwHead];
-    }
-    const int Nd = n0 + n1 + n2;
-    int d0, d1;
-    dense_range(a, split, d0, d1);
+    const int Nd = dv.Nd;
     float* my = dl + wave * GP * (2 + kMfD);
 #pragma unroll 1
     for (int pass = 0; pass < NPASS; ++pass) {
         const int gb = pass * HP;
-        float q[HP][8];
-#pragma unroll
-        for (int g = 0; g < HP; ++g) {
-            if (gb + g < gc) {
-                load_f32<8>(in.Q + static_cast<size_t>(kvh * G + g0 + gb + g) * kMfD + cp * 8, q[g]);
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) q[g][j] = 0.0f;
-            }
-        }
         float m[HP], l[HP], acc[HP][8];
 #pragma unroll
         for (int g = 0; g < HP; ++g) {
@@ -225,37 +281,28 @@ __device__ __forceinline__ void dense_share(const SplitArgs& a, const int split,
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
         }
-        for (int k = d0 + wave; k < d1; k += 4) {
+        // One tile into the running (m, l, acc) of the pass's heads.
+        auto consume = [&](const DenseTile& t, const int k) {
             const int tok0 = 16 * k + 4 * tg;
-            float kx[4][8], vx[4][8];
-            bool valid[4];
-            // Rows past the tiers repeat the last row (finite data, masked below).
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r0 = tok0 + i;
-                valid[i] = r0 < Nd;
-                const int r = valid[i] ? r0 : Nd - 1;
-                const bool in0 = r < n0, in1 = r < n0 + n1;
-                int ring = head + (r - n0 - n1);
-                ring = ring >= in.ring_size ? ring - in.ring_size : ring;
-                const int idx = in0 ? r : (in1 ? r - n0 : ring);
-                const float* kb = in0 ? in.k0 : (in1 ? in.k1 : in.k2);
-                const float* vb = in0 ? in.v0 : (in1 ? in.v1 : in.v2);
-                const int off = (idx * Hkv + kvh) * kMfD + cp * 8;
-                load_f32<8>(kb + off, kx[i]);
-                load_f32<8>(vb + off, vx[i]);
-            }
             float s[4][HP];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int g = 0; g < HP; ++g) {
+                // read here, one head at a time (an opaque offset keeps the
+                // compiler from holding all heads in registers)
+                int qo = (gb + g) * kMfD + cp * 8;
+                asm volatile("" : "+v"(qo));
+                const float4 qa = *reinterpret_cast<const float4*>(q_l + qo);
+                const float4 qb = *reinterpret_cast<const float4*>(q_l + qo + 4);
+                const float qg[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
 #pragma unroll
-                for (int g = 0; g < HP; ++g) {
+                for (int i = 0; i < 4; ++i) {
                     float d = 0.0f;
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) d = __builtin_fmaf(q[g][j], kx[i][j], d);
-                    const float t = row_sum16(d) * a.scale2;
-                    s[i][g] = valid[i] ? t : kNegInf;
+                    for (int j = 0; j < 8; ++j) d = __builtin_fmaf(qg[j], t.kx[i][j], d);
+                    const float v = row_sum16(d) * a.scale2;
+                    s[i][g] = (tok0 + i < Nd) ? v : kNegInf;
                 }
+            }
             if (a.logits) {
 #pragma unroll
                 for (int g = 0; g < HP; ++g) {
@@ -266,7 +313,7 @@ __device__ __forceinline__ void dense_share(const SplitArgs& a, const int split,
                         } else {
 #pragma unroll
                             for (int i = 0; i < 4; ++i)
-                                if (valid[i]) lr[i] = s[i][g];
+                                if (tok0 + i < Nd) lr[i] = s[i][g];
                         }
                     }
                 }
@@ -284,14 +331,30 @@ __device__ __forceinline__ void dense_share(const SplitArgs& a, const int split,
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     float v = acc[g][j] * alpha;
-                    v = __builtin_fmaf(p[0], vx[0][j], v);
-                    v = __builtin_fmaf(p[1], vx[1][j], v);
-                    v = __builtin_fmaf(p[2], vx[2][j], v);
-                    v = __builtin_fmaf(p[3], vx[3][j], v);
+                    v = __builtin_fmaf(p[0], t.vx[0][j], v);
+                    v = __builtin_fmaf(p[1], t.vx[1][j], v);
+                    v = __builtin_fmaf(p[2], t.vx[2][j], v);
+                    v = __builtin_fmaf(p[3], t.vx[3][j], v);
                     acc[g][j] = v;
                 }
                 m[g] = mn;
             }
+        };
+        const int kf = d0 + wave;
+        if (kf < d1) {
+            if (pass == 0) {
+                consume(t0, kf);  // in flight since the start of the kernel
+            } else {
+                DenseTile t;
+                dense_load(in, dv, kvh, kf, t);
+                consume(t, kf);
+            }
+        }
+#pragma unroll 1
+        for (int k = kf + 4; k < d1; k += 4) {
+            DenseTile t;
+            dense_load(in, dv, kvh, k, t);
+            consume(t, k);
         }
         // Sum the four row groups (they share m) and leave the partial in LDS.
 #pragma unroll
@@ -312,10 +375,55 @@ __device__ __forceinline__ void dense_share(const SplitArgs& a, const int split,
     }
 }
 
-// One workgroup: KV head blockIdx.y, query heads [GP * blockIdx.z, +GP), a
-// contiguous range of 32-token pairs of packed tiles and a share of the FP32
-// tiles; each wave takes a contiguous sub-range of the pairs. Writes partial
-// slot `split` of each head.
+// One FP32-tier workgroup: KV head blockIdx.y, query heads [GP * blockIdx.z,
+// +GP), FP32 tiles [d0, d1) of share `dsplit`. The four waves' partials merge
+// in LDS into partial slot nsplit_p + dsplit of each head.
+template <int GP>
+__device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit, char* lds) {
+    using L = DnLds<GP>;
+    const AttnInputs& in = a.in;
+    const int kvh = blockIdx.y;
+    const int G = in.Hq / in.Hkv;
+    const int g0 = blockIdx.z * GP;
+    const int gc = min(GP, G - g0);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const DenseView dv = dense_view(in);
+    int d0, d1;
+    dense_range(a, dv.Nd, dsplit, d0, d1);
+    float* q_l = reinterpret_cast<float*>(lds + L::QL);
+    float* dl = reinterpret_cast<float*>(lds + L::PART);
+    load_q_lds<GP>(in, kvh, g0, gc, q_l);
+    DenseTile dt;
+    if (d0 + wave < d1) dense_load(in, dv, kvh, d0 + wave, dt);
+    __syncthreads();
+    dense_share<GP>(a, dv, d0, d1, kvh, g0, gc, wave, q_l, dt, dl);
+    __syncthreads();
+    const int split = a.nsplit_p + dsplit;
+    for (int idx = threadIdx.x; idx < gc * kMfD; idx += 256) {
+        const int g = idx / kMfD, c = idx - g * kMfD;
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, dl[(w * GP + g) * (2 + kMfD)]);
+        float A = 0.0f, Ls = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            const float* dg = dl + (w * GP + g) * (2 + kMfD);
+            const float f = (dg[0] == kNegInf) ? 0.0f : exp2f(dg[0] - M);  // waves without tiles add nothing
+            A = __builtin_fmaf(f, dg[2 + c], A);
+            Ls = __builtin_fmaf(f, dg[1], Ls);
+        }
+        const size_t pi = static_cast<size_t>(kvh * G + g0 + g) * a.nsplit + split;
+        a.part_acc[pi * kMfD + c] = A;
+        if (c == 0) {
+            a.part_ml[2 * pi] = (Ls > 0.0f) ? M : kNegInf;
+            a.part_ml[2 * pi + 1] = Ls;
+        }
+    }
+}
+
+// One packed workgroup: KV head blockIdx.y, query heads [GP * blockIdx.z,
+// +GP), a contiguous range of 32-token pairs of packed tiles; each wave takes
+// a contiguous quarter of it. Writes partial slot `split` of each head.
 //
 // The high and low f16 halves of the QK coefficients sit in MFMA columns
 // h and h + 8, so one MFMA per 32 channels yields both products; a DPP
@@ -367,10 +475,50 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     float* bias_l = reinterpret_cast<float*>(wl + L::BIAS);
     char* bhl_l = wl + L::BHL;
 
-    // The workgroup's share of the FP32 tiers first, before the packed loop's
-    // registers are live.
-    float* dl = reinterpret_cast<float*>(lds + L::DENSE);
-    dense_share<GP>(a, split, kvh, g0, gc, wave, dl);
+    // The query heads first (the barrier below waits for them only), then the
+    // wave's first pair of packed tiles, whose latency overlaps theirs.
+    float* q_l = reinterpret_cast<float*>(lds + L::QL);
+    load_q_lds<GP>(in, kvh, g0, gc, q_l);
+    const int32_t* kp_h = in.kp + kvh * kMfD;
+    const MetaT* ks_h = static_cast<const MetaT*>(in.ks) + kvh * kMfD;
+    const MetaT* kz_h = static_cast<const MetaT*>(in.kz) + kvh * kMfD;
+    const int32_t* vp_h = in.vp + kvh * (kMfD / 16);
+    const MetaT* vm_h = static_cast<const MetaT*>(lane < 32 ? in.vs : in.vz) + kvh;
+    const int lk = 4 * (lane & 31);
+    const int tv = 4 * (lane >> 3) + (lane & 3);
+    const int hfo = 4 * ((lane >> 2) & 1);
+    const int t2 = lane & 31;
+
+    // Registers of the pair being fetched.
+    mf_u4 kw, vw;
+    float4 ksr, kzr;
+    float vm = 0.0f;
+    long long idv = -1;
+    bool okv = false;
+
+    auto fetch = [&](const int p) {
+        const int kt0 = 2 * p;
+        const int kto = min(lane >> 5, Tp - 1 - kt0);  // 0 when the pair has a single tile
+        kw = *reinterpret_cast<const mf_u4*>(kp_h + static_cast<size_t>(kt0) * tstride + (kto * tstride + lk));
+        const int bb = (W == 2) ? p : kt0;
+        const int bo = (W == 2) ? 0 : kto;
+        const size_t mb = static_cast<size_t>(bb) * tstride;
+        ksr = load_meta4<MetaT>(ks_h + mb + (bo * tstride + lk));
+        kzr = load_meta4<MetaT>(kz_h + mb + (bo * tstride + lk));
+        const int s0 = 32 * p;
+        const int lim = nslots - 1 - s0;
+        vw = *reinterpret_cast<const mf_u4*>(vp_h + static_cast<size_t>(s0) * vstride + (min(tv, lim) * vstride + hfo));
+        const int ts = min(t2, lim);
+        vm = Meta<MetaT>::load(vm_h + static_cast<size_t>(s0) * Hkv, static_cast<size_t>(ts * Hkv));
+        idv = in.ids[s0 + ts];
+        okv = t2 <= lim;
+    };
+
+    // this wave's quarter of the workgroup's pairs
+    const int wp0 = pb + part_begin(pe - pb, wave, 4);
+    const int wp1 = pb + part_begin(pe - pb, wave + 1, 4);
+    if (wp0 < wp1) fetch(wp0);
+    __syncthreads();
 
     // Q' = Q 2^-e per head (e = exponent of max |Q_h|) in the coefficient
     // layout: pass pp, head 4 pp + gk, channels 8 n .. 8 n + 7.
@@ -379,15 +527,16 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
         const int h = 4 * pp + gk;
-        if (h < gc) {
-            const float* qp = in.Q + static_cast<size_t>(kvh * G + g0 + h) * kMfD + 8 * n;
+        {
+            // heads past gc are zero in q_l
+            const float* qp = q_l + (h < GP ? h : 0) * kMfD + 8 * n;
             const float4 x0 = *reinterpret_cast<const float4*>(qp);
             const float4 x1 = *reinterpret_cast<const float4*>(qp + 4);
-            qv[pp][0] = x0.x; qv[pp][1] = x0.y; qv[pp][2] = x0.z; qv[pp][3] = x0.w;
-            qv[pp][4] = x1.x; qv[pp][5] = x1.y; qv[pp][6] = x1.z; qv[pp][7] = x1.w;
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) qv[pp][j] = 0.0f;
+            const bool hv = h < GP;
+            qv[pp][0] = hv ? x0.x : 0.0f; qv[pp][1] = hv ? x0.y : 0.0f;
+            qv[pp][2] = hv ? x0.z : 0.0f; qv[pp][3] = hv ? x0.w : 0.0f;
+            qv[pp][4] = hv ? x1.x : 0.0f; qv[pp][5] = hv ? x1.y : 0.0f;
+            qv[pp][6] = hv ? x1.z : 0.0f; qv[pp][7] = hv ? x1.w : 0.0f;
         }
         float mx = 0.0f;
 #pragma unroll
@@ -417,45 +566,10 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     const uint32_t qsel1 = (lane & 1) ? 0x03070105u : 0x06020400u;
     const uint32_t qsel2 = (lane & 2) ? 0x03020706u : 0x05040100u;
 
-    const int32_t* kp_h = in.kp + kvh * kMfD;
-    const MetaT* ks_h = static_cast<const MetaT*>(in.ks) + kvh * kMfD;
-    const MetaT* kz_h = static_cast<const MetaT*>(in.kz) + kvh * kMfD;
-    const int32_t* vp_h = in.vp + kvh * (kMfD / 16);
-    const MetaT* vm_h = static_cast<const MetaT*>(lane < 32 ? in.vs : in.vz) + kvh;
-    const int lk = 4 * (lane & 31);
-    const int tv = 4 * (lane >> 3) + (lane & 3);
-    const int hfo = 4 * ((lane >> 2) & 1);
-    const int t2 = lane & 31;
-
     mf_f4 acc[8];
 #pragma unroll
     for (int s = 0; s < 8; ++s) acc[s] = mf_f4{0.0f, 0.0f, 0.0f, 0.0f};
     float m_run = -1.0e30f, l_run = 0.0f, pz = 0.0f;
-
-    // Registers of the pair being fetched.
-    mf_u4 kw, vw;
-    float4 ksr, kzr;
-    float vm = 0.0f;
-    long long idv = -1;
-    bool okv = false;
-
-    auto fetch = [&](const int p) {
-        const int kt0 = 2 * p;
-        const int kto = min(lane >> 5, Tp - 1 - kt0);  // 0 when the pair has a single tile
-        kw = *reinterpret_cast<const mf_u4*>(kp_h + static_cast<size_t>(kt0) * tstride + (kto * tstride + lk));
-        const int bb = (W == 2) ? p : kt0;
-        const int bo = (W == 2) ? 0 : kto;
-        const size_t mb = static_cast<size_t>(bb) * tstride;
-        ksr = load_meta4<MetaT>(ks_h + mb + (bo * tstride + lk));
-        kzr = load_meta4<MetaT>(kz_h + mb + (bo * tstride + lk));
-        const int s0 = 32 * p;
-        const int lim = nslots - 1 - s0;
-        vw = *reinterpret_cast<const mf_u4*>(vp_h + static_cast<size_t>(s0) * vstride + (min(tv, lim) * vstride + hfo));
-        const int ts = min(t2, lim);
-        vm = Meta<MetaT>::load(vm_h + static_cast<size_t>(s0) * Hkv, static_cast<size_t>(ts * Hkv));
-        idv = in.ids[s0 + ts];
-        okv = t2 <= lim;
-    };
 
     // Lays the fetched pair out in LDS; returns the token-validity mask.
     auto stage = [&]() -> uint32_t {
@@ -464,26 +578,26 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         const uint32_t u1 = __builtin_amdgcn_perm(kw.y, kw.x, 0x07030602u);
         const uint32_t v0 = __builtin_amdgcn_perm(kw.w, kw.z, 0x05010400u);
         const uint32_t v1 = __builtin_amdgcn_perm(kw.w, kw.z, 0x07030602u);
-        uint32_t* kd = kt_l + (lane >> 5) * 128 + (lane & 31);
+        uint32_t* kd = kt_l + (lane >> 5) * 4 * kKTS + (lane & 31);
         kd[0] = __builtin_amdgcn_perm(v0, u0, 0x05040100u);
-        kd[32] = __builtin_amdgcn_perm(v0, u0, 0x07060302u);
-        kd[64] = __builtin_amdgcn_perm(v1, u1, 0x05040100u);
-        kd[96] = __builtin_amdgcn_perm(v1, u1, 0x07060302u);
+        kd[kKTS] = __builtin_amdgcn_perm(v0, u0, 0x07060302u);
+        kd[2 * kKTS] = __builtin_amdgcn_perm(v1, u1, 0x05040100u);
+        kd[3 * kKTS] = __builtin_amdgcn_perm(v1, u1, 0x07060302u);
         // V: 4x4 byte transpose across the quad (tokens 4m..4m+3).
         const int m = lane >> 3;
         const int hf = (lane >> 2) & 1;
-        uint32_t* vd = vt_l + (16 * hf + (lane & 3)) * 8 + 2 * (m & 3) + (m >> 2);
+        uint32_t* vd = vt_l + (16 * hf + (lane & 3)) * kVTS + 2 * (m & 3) + (m >> 2);
         const uint32_t vwv[4] = {vw.x, vw.y, vw.z, vw.w};
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const uint32_t x = vwv[g];
             const uint32_t t = __builtin_amdgcn_perm(dpp_u32_quad1(x), x, qsel1);
             const uint32_t y = __builtin_amdgcn_perm(dpp_u32_quad2(t), t, qsel2);
-            vd[g * 32] = y;  // byte column 4 (4 hf + g) + (lane & 3)
+            vd[g * 4 * kVTS] = y;  // byte column 4 (4 hf + g) + (lane & 3)
         }
-        float* kzd = ksz_l + (lane >> 5) * 256 + lk;
+        float* kzd = ksz_l + (lane >> 5) * 2 * kKSZ + lk + 4 * ((lane & 31) >> 3);
         *reinterpret_cast<float4*>(kzd) = ksr;
-        *reinterpret_cast<float4*>(kzd + 128) = kzr;
+        *reinterpret_cast<float4*>(kzd + kKSZ) = kzr;
         const bool ok = okv && idv != -1;
         const int pos = 8 * ((t2 & 15) >> 2) + 4 * (t2 >> 4) + (t2 & 3);
         (lane < 32 ? vs_l : vz_l)[pos] = ok ? vm : 0.0f;  // masked slots contribute nothing
@@ -496,11 +610,11 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
 #pragma unroll
         for (int pp = 0; pp < NP; ++pp) {
             const int h = 4 * pp + gk;
-            const float* kss = ksz_l + tile * 256 + 8 * n;
+            const float* kss = ksz_l + tile * 2 * kKSZ + 8 * n + 4 * (n >> 2);
             const float4 sa = *reinterpret_cast<const float4*>(kss);
             const float4 sb = *reinterpret_cast<const float4*>(kss + 4);
-            const float4 za = *reinterpret_cast<const float4*>(kss + 128);
-            const float4 zb = *reinterpret_cast<const float4*>(kss + 132);
+            const float4 za = *reinterpret_cast<const float4*>(kss + kKSZ);
+            const float4 zb = *reinterpret_cast<const float4*>(kss + kKSZ + 4);
             const float sc[8] = {sa.x, sa.y, sa.z, sa.w, sb.x, sb.y, sb.z, sb.w};
             const float zc[8] = {za.x, za.y, za.z, za.w, zb.x, zb.y, zb.z, zb.w};
             float av[8];
@@ -514,44 +628,14 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
             split_hl4(av[0], av[2], av[1], av[3], av[4], av[6], av[5], av[7], hi, lo);
             bp = row_sum16(bp);
             if (GP >= 4 || h < GP) {
-                *reinterpret_cast<mf_u4*>(bt + (h * kMfD + 8 * n) * 2) = hi;
-                *reinterpret_cast<mf_u4*>(bt + ((GP + h) * kMfD + 8 * n) * 2) = lo;
+                *reinterpret_cast<mf_u4*>(bt + (h * kBRS + 8 * n) * 2) = hi;
+                *reinterpret_cast<mf_u4*>(bt + ((GP + h) * kBRS + 8 * n) * 2) = lo;
                 if (n == 0) bias_l[tile * 8 + h] = bp;
             }
         }
     };
 
-    // Contiguous pair range of this wave: the wave's FP32 tiles (round-robin,
-    // ~kDenseCost pairs each) plus its pairs even out over the four waves.
-    int wp0 = pb, wp1 = pe;
-    {
-        constexpr int kDenseCost = 3;
-        int d0, d1;
-        dense_range(a, split, d0, d1);
-        const int nd = d1 - d0;
-        const int np = pe - pb;
-        // budgets of waves [0, wave) and of this wave (no indexed arrays:
-        // the compiler would move one into LDS per thread)
-        int before = 0, mine = 0, S = 0;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int cd = nd > v ? (nd - v + 3) / 4 : 0;
-            const int share = (nd * kDenseCost + np + 3 - v) / 4;
-            const int b = max(0, share - cd * kDenseCost);
-            before += (v < wave) ? b : 0;
-            mine = (v == wave) ? b : mine;
-            S += b;
-        }
-        if (S > 0) {
-            wp0 = pb + part_begin(np, before, S);
-            wp1 = pb + part_begin(np, before + mine, S);
-        } else {
-            wp0 = wave == 3 ? pb : pe;
-        }
-    }
-    int p = wp0;
-    if (p < wp1) fetch(p);
-    for (; p < wp1; ++p) {
+    for (int p = wp0; p < wp1; ++p) {
         const uint32_t vmask = stage();
         if (p + 1 < wp1) fetch(p + 1);
         wave_lds_sync();
@@ -564,9 +648,9 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         for (int tile = 0; tile < 2; ++tile) {
             const int tb = (W == 2) ? 0 : tile;
             // A: codes of token t = lane & 15 (k = t & 3), channels 32 gk .. 32 gk + 31.
-            const mf_u4* ka = reinterpret_cast<const mf_u4*>(kt_l + (tile * 4 + ((lane & 15) >> 2)) * 32 + 8 * gk);
+            const mf_u4* ka = reinterpret_cast<const mf_u4*>(kt_l + (tile * 4 + ((lane & 15) >> 2)) * kKTS + 8 * gk);
             const mf_u4 ra = ka[0], rb = ka[1];
-            const mf_u4* kb = reinterpret_cast<const mf_u4*>(bhl_l + tb * L::BHL_TILE + (brow * kMfD + 32 * gk) * 2);
+            const mf_u4* kb = reinterpret_cast<const mf_u4*>(bhl_l + tb * L::BHL_TILE + (brow * kBRS + 32 * gk) * 2);
             mf_f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
@@ -655,8 +739,8 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         // B: codes of channel 4 beta + k for the lane's 8 tokens,
         // beta = n (nsteps 0..3) and n + 16 (nsteps 4..7), k = nstep & 3.
         const uint2* vtr = reinterpret_cast<const uint2*>(vt_l);
-        const uint2 q0 = vtr[n * 4 + gk];
-        const uint2 q1 = vtr[(n + 16) * 4 + gk];
+        const uint2 q0 = vtr[n * (kVTS / 2) + gk];
+        const uint2 q1 = vtr[(n + 16) * (kVTS / 2) + gk];
         const uint32_t q0a = q0.x >> 8, q0b = q0.y >> 8, q1a = q1.x >> 8, q1b = q1.y >> 8;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -706,17 +790,14 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         const int g = idx / kMfD, c = idx - g * kMfD;
         float M = -1.0e30f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, fmaxf(sm_m[w * GP + g], dl[(w * GP + g) * (2 + kMfD)]));
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w * GP + g]);
         float A = 0.0f, Ls = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
+            // a wave without pairs has m = -1e30, l = 0, acc = 0: it adds nothing
             const float f = exp2f(sm_m[w * GP + g] - M);
             A = __builtin_fmaf(f, sm_acc[(w * GP + g) * kMfD + c] + sm_z[w * GP + g], A);
             Ls = __builtin_fmaf(f, sm_l[w * GP + g], Ls);
-            const float* dg = dl + (w * GP + g) * (2 + kMfD);
-            const float fd = (dg[0] == kNegInf) ? 0.0f : exp2f(dg[0] - M);
-            A = __builtin_fmaf(fd, dg[2 + c], A);
-            Ls = __builtin_fmaf(fd, dg[1], Ls);
         }
         const size_t pi = static_cast<size_t>(kvh * G + g0 + g) * a.nsplit + split;
         a.part_acc[pi * kMfD + c] = A;
