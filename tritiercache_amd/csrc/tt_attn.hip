@@ -390,29 +390,31 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
 
 #include "tt_attn_mfma.h"
 
-// head_dim 128: grid (nsplit_p + nsplit_d) x Hkv x head chunks. Workgroups
-// x < nsplit_p run the matrix-core loop over the packed store, the others a
-// VALU pass over a share of the FP32 tiers; every workgroup writes its own
-// partial slot.
+// head_dim 128: a 1-D grid of ceil(nsplit / 8) * 8 slots per (KV head, head
+// chunk). Slots s < nsplit_p run the matrix-core loop over pair range s of
+// the packed store, slots nsplit_p <= s < nsplit a VALU pass over a share of
+// the FP32 tiers; every workgroup writes its own partial slot.
+//
+// Workgroup ids go round-robin over the 8 XCDs (id % 8), each with its own
+// L2. The id -> (slot, head) map puts slot s on XCD s % 8 for every head and
+// dispatches the heads of one slot back to back: a token's V words, V scale /
+// zero and id sit in the same 128-byte lines for all KV heads, so they come
+// from memory once per token instead of once per head.
 template <int GP, typename MetaT>
-__global__ void __launch_bounds__(256) attn_packed_kernel(SplitArgs a) {
+__global__ void __launch_bounds__(256) attn_packed_kernel(SplitArgs a, const int hc, const int chunks) {
     constexpr int kLds = MfLds<GP>::TOTAL > DnLds<GP>::TOTAL ? MfLds<GP>::TOTAL : DnLds<GP>::TOTAL;
     __shared__ __align__(16) char lds[kLds];
-    const int bx = static_cast<int>(blockIdx.x);
-    if (bx >= a.nsplit_p) {
-        dense_body<GP>(a, bx - a.nsplit_p, lds);
+    const unsigned id = blockIdx.x;
+    const unsigned q = id >> 3;
+    const int hz = static_cast<int>(q % static_cast<unsigned>(hc));  // (KV head, chunk)
+    const int s = static_cast<int>((q / static_cast<unsigned>(hc)) * 8 + (id & 7));
+    if (s >= a.nsplit) return;  // padding slot of the last group of 8
+    const int kvh = hz / chunks, chunk = hz - kvh * chunks;
+    if (s >= a.nsplit_p) {
+        dense_body<GP>(a, s - a.nsplit_p, kvh, chunk, lds);
         return;
     }
-    // The KV heads of one tile sit side by side in memory (512-byte K rows,
-    // 32-byte V rows): rotate each head's split index so the workgroups that
-    // run together stream different regions instead of the same DRAM pages.
-    const int heads = static_cast<int>(gridDim.y * gridDim.z);
-    const int hid = static_cast<int>(blockIdx.y * gridDim.z + blockIdx.z);
-    const int rot = static_cast<int>(static_cast<unsigned>(a.nsplit_p) * static_cast<unsigned>(hid) /
-                                     static_cast<unsigned>(heads));
-    int split = bx + rot;
-    split = split >= a.nsplit_p ? split - a.nsplit_p : split;
-    packed_body<GP, MetaT>(a, __builtin_amdgcn_readfirstlane(split), lds);
+    packed_body<GP, MetaT>(a, s, kvh, chunk, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -730,22 +732,28 @@ int launch_split_g(const SplitArgs& a, dim3 grid, int gp, int meta_fp16, hipStre
     }
 }
 
+// Grid of attn_packed_kernel: ceil(nsplit / 8) groups of 8 slots for each
+// (KV head, head chunk).
 template <int GP>
-int launch_packed_meta(const SplitArgs& a, dim3 grid, int meta_fp16, hipStream_t st) {
+int launch_packed_meta(const SplitArgs& a, int Hkv, int chunks, int meta_fp16, hipStream_t st) {
+    const int hc = Hkv * chunks;
+    const long long wgs = static_cast<long long>((a.nsplit + 7) / 8) * 8 * hc;
+    if (wgs > 0x7fffffffLL) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "attention grid too large");
+    const dim3 grid(static_cast<unsigned>(wgs));
     if (meta_fp16)
-        hipLaunchKernelGGL((attn_packed_kernel<GP, uint16_t>), grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((attn_packed_kernel<GP, uint16_t>), grid, dim3(256), 0, st, a, hc, chunks);
     else
-        hipLaunchKernelGGL((attn_packed_kernel<GP, float>), grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL((attn_packed_kernel<GP, float>), grid, dim3(256), 0, st, a, hc, chunks);
     TT_LAUNCH_CHECK();
     return TT_OK;
 }
 
-int launch_packed(const SplitArgs& a, dim3 grid, int gp, int meta_fp16, hipStream_t st) {
+int launch_packed(const SplitArgs& a, int Hkv, int chunks, int gp, int meta_fp16, hipStream_t st) {
     switch (gp) {
-    case 1: return launch_packed_meta<1>(a, grid, meta_fp16, st);
-    case 2: return launch_packed_meta<2>(a, grid, meta_fp16, st);
-    case 4: return launch_packed_meta<4>(a, grid, meta_fp16, st);
-    default: return launch_packed_meta<8>(a, grid, meta_fp16, st);
+    case 1: return launch_packed_meta<1>(a, Hkv, chunks, meta_fp16, st);
+    case 2: return launch_packed_meta<2>(a, Hkv, chunks, meta_fp16, st);
+    case 4: return launch_packed_meta<4>(a, Hkv, chunks, meta_fp16, st);
+    default: return launch_packed_meta<8>(a, Hkv, chunks, meta_fp16, st);
     }
 }
 
@@ -897,7 +905,7 @@ int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipS
     const int chunks = (G + gp - 1) / gp;
     if (use_packed_kernel(in.D)) {
         if (plan.nsplit_p <= 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
-        return launch_packed(a, dim3(plan.nsplit, in.Hkv, chunks), gp, in.meta_fp16, stream);
+        return launch_packed(a, in.Hkv, chunks, gp, in.meta_fp16, stream);
     }
     const dim3 grid(plan.nsplit, in.Hkv, chunks);
     if (plan.nsplit_p != 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");

@@ -110,11 +110,12 @@ __device__ __forceinline__ float row_max16(float x) {
     return x;
 }
 
+// Quad permutations (every lane reads a valid source, so no old value).
 __device__ __forceinline__ uint32_t dpp_u32_quad1(uint32_t x) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0xB1, 0xF, 0xF, false));
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xB1, 0xF, 0xF, true));
 }
 __device__ __forceinline__ uint32_t dpp_u32_quad2(uint32_t x) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(x), 0x4E, 0xF, 0xF, false));
+    return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0x4E, 0xF, 0xF, true));
 }
 
 // Orders this wave's LDS writes before its later LDS reads of other lanes'
@@ -140,16 +141,38 @@ __device__ __forceinline__ uint32_t code_f16(uint32_t x, uint32_t mk, uint32_t o
     return __builtin_bit_cast(uint32_t, v - off);
 }
 
-// x0, x1 -> (hi, lo) f16 pairs with x ~= hi + lo: hi truncated, lo the
-// rounded-to-nearest remainder (exact in f32).
+// x - m * f16 (low / high half of h), one v_fma_mix_f32 (exact for m = 1
+// and h a rounding of x: the difference fits in f32).
+__device__ __forceinline__ float fma_mix_lo(uint32_t h, float negm, float x) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(negm), "v"(x));
+    return r;
+}
+__device__ __forceinline__ float fma_mix_hi(uint32_t h, float negm, float x) {
+    float r;
+    asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h), "v"(negm), "v"(x));
+    return r;
+}
+
+__device__ __forceinline__ uint32_t cvt_pk_f16(float x0, float x1) {
+    mf_h2 v;
+    v.x = static_cast<_Float16>(x0);
+    v.y = static_cast<_Float16>(x1);
+    return __builtin_bit_cast(uint32_t, v);
+}
+
+// x0, x1 -> (hi, lo) f16 pairs with x ~= hi + lo: hi and the remainder lo
+// both rounded to nearest (the remainder is exact in f32).
 __device__ __forceinline__ uint2 split_hl(float x0, float x1) {
-    const mf_h2 h = __builtin_bit_cast(mf_h2, __builtin_amdgcn_cvt_pkrtz(x0, x1));
-    const float r0 = x0 - static_cast<float>(h.x);
-    const float r1 = x1 - static_cast<float>(h.y);
-    mf_h2 l;
-    l.x = static_cast<_Float16>(r0);
-    l.y = static_cast<_Float16>(r1);
-    return make_uint2(__builtin_bit_cast(uint32_t, h), __builtin_bit_cast(uint32_t, l));
+    const uint32_t hi = cvt_pk_f16(x0, x1);
+    return make_uint2(hi, cvt_pk_f16(fma_mix_lo(hi, -1.0f, x0), fma_mix_hi(hi, -1.0f, x1)));
+}
+
+// One half of the split per lane: hi where negm = 0, lo where negm = -1
+// (the rounding of x, then of its remainder, exactly as split_hl).
+__device__ __forceinline__ uint32_t split_half(float x0, float x1, float negm) {
+    const uint32_t hi = cvt_pk_f16(x0, x1);
+    return cvt_pk_f16(fma_mix_lo(hi, negm, x0), fma_mix_hi(hi, negm, x1));
 }
 
 // Four split pairs -> (hi operand, lo operand).
@@ -375,16 +398,16 @@ __device__ __forceinline__ void dense_share(const SplitArgs& a, const DenseView&
     }
 }
 
-// One FP32-tier workgroup: KV head blockIdx.y, query heads [GP * blockIdx.z,
-// +GP), FP32 tiles [d0, d1) of share `dsplit`. The four waves' partials merge
-// in LDS into partial slot nsplit_p + dsplit of each head.
+// One FP32-tier workgroup: KV head kvh, query heads [GP * chunk, +GP), FP32
+// tiles [d0, d1) of share `dsplit`. The four waves' partials merge in LDS
+// into partial slot nsplit_p + dsplit of each head.
 template <int GP>
-__device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit, char* lds) {
+__device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit, const int kvh, const int chunk,
+                                           char* lds) {
     using L = DnLds<GP>;
     const AttnInputs& in = a.in;
-    const int kvh = blockIdx.y;
     const int G = in.Hq / in.Hkv;
-    const int g0 = blockIdx.z * GP;
+    const int g0 = chunk * GP;
     const int gc = min(GP, G - g0);
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const DenseView dv = dense_view(in);
@@ -421,9 +444,9 @@ __device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit,
     }
 }
 
-// One packed workgroup: KV head blockIdx.y, query heads [GP * blockIdx.z,
-// +GP), a contiguous range of 32-token pairs of packed tiles; each wave takes
-// a contiguous quarter of it. Writes partial slot `split` of each head.
+// One packed workgroup: KV head kvh, query heads [GP * chunk, +GP), a
+// contiguous range of 32-token pairs of packed tiles; each wave takes a
+// contiguous quarter of it. Writes partial slot `split` of each head.
 //
 // The high and low f16 halves of the QK coefficients sit in MFMA columns
 // h and h + 8, so one MFMA per 32 channels yields both products; a DPP
@@ -432,14 +455,14 @@ __device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit,
 // row h and low in row h + 8; the two accumulator rows are added once at the
 // end. Columns / rows of padding heads repeat head 0 and are never stored.
 template <int GP, typename MetaT>
-__device__ __forceinline__ void packed_body(const SplitArgs& a, const int split, char* lds) {
+__device__ __forceinline__ void packed_body(const SplitArgs& a, const int split, const int kvh, const int chunk,
+                                            char* lds) {
     static_assert(GP >= 1 && GP <= 8, "at most 8 query heads per workgroup");
     constexpr int NP = GP >= 4 ? GP / 4 : 1;  // coefficient passes (4 heads x 16 chunks each)
     using L = MfLds<GP>;
     const AttnInputs& in = a.in;
-    const int kvh = blockIdx.y;
     const int G = in.Hq / in.Hkv;
-    const int g0 = blockIdx.z * GP;
+    const int g0 = chunk * GP;
     const int gc = min(GP, G - g0);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar loop control
@@ -447,6 +470,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     const int gk = lane >> 4;  // MFMA reduction group
     const int hn = n & 7;      // query head of column n
     const bool lo_col = n >= 8;
+    const float negm_col = lo_col ? -1.0f : 0.0f;  // PV operand: lo rows take the remainder
     const int Hkv = in.Hkv;
 
     int n0 = in.n0, n1 = in.n1, n2 = in.n2, nb = in.num_blocks;
@@ -489,6 +513,24 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     const int hfo = 4 * ((lane >> 2) & 1);
     const int t2 = lane & 31;
 
+    // Per-lane element offsets of a pair's loads from the pair's base
+    // addresses: those of a whole pair, and those of the store's last pair,
+    // which may hold one tile (kto = 0 for both halves) and fewer slots
+    // (lanes past the end re-read the last slot and are masked).
+    struct PairOffs {
+        uint32_t k, km, v, vm, id;
+    };
+    auto pair_offs = [&](const int kto, const int lim) {
+        const int ts = min(t2, lim);
+        return PairOffs{static_cast<uint32_t>(kto * tstride + lk),
+                        static_cast<uint32_t>(((W == 2) ? 0 : kto) * tstride + lk),
+                        static_cast<uint32_t>(min(tv, lim) * vstride + hfo), static_cast<uint32_t>(ts * Hkv),
+                        static_cast<uint32_t>(ts)};
+    };
+    const PairOffs off_full = pair_offs(lane >> 5, 31);
+    const int lim_last = nslots - 1 - 32 * (P - 1);
+    const PairOffs off_last = pair_offs(min(lane >> 5, Tp - 1 - 2 * (P - 1)), lim_last);
+
     // Registers of the pair being fetched.
     mf_u4 kw, vw;
     float4 ksr, kzr;
@@ -496,22 +538,26 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     long long idv = -1;
     bool okv = false;
 
+    // Wave-uniform bases (scalar) plus the per-lane offsets.
+    auto fetch_at = [&](const int p, const PairOffs& o) {
+        const size_t kb = static_cast<size_t>(2 * p) * tstride;
+        const size_t mb = static_cast<size_t>((W == 2) ? p : 2 * p) * tstride;
+        const size_t s0 = static_cast<size_t>(32 * p);
+        kw = *reinterpret_cast<const mf_u4*>(kp_h + kb + o.k);
+        ksr = load_meta4<MetaT>(ks_h + mb + o.km);
+        kzr = load_meta4<MetaT>(kz_h + mb + o.km);
+        vw = *reinterpret_cast<const mf_u4*>(vp_h + s0 * vstride + o.v);
+        vm = Meta<MetaT>::load(vm_h + s0 * Hkv, o.vm);
+        idv = in.ids[s0 + o.id];
+    };
     auto fetch = [&](const int p) {
-        const int kt0 = 2 * p;
-        const int kto = min(lane >> 5, Tp - 1 - kt0);  // 0 when the pair has a single tile
-        kw = *reinterpret_cast<const mf_u4*>(kp_h + static_cast<size_t>(kt0) * tstride + (kto * tstride + lk));
-        const int bb = (W == 2) ? p : kt0;
-        const int bo = (W == 2) ? 0 : kto;
-        const size_t mb = static_cast<size_t>(bb) * tstride;
-        ksr = load_meta4<MetaT>(ks_h + mb + (bo * tstride + lk));
-        kzr = load_meta4<MetaT>(kz_h + mb + (bo * tstride + lk));
-        const int s0 = 32 * p;
-        const int lim = nslots - 1 - s0;
-        vw = *reinterpret_cast<const mf_u4*>(vp_h + static_cast<size_t>(s0) * vstride + (min(tv, lim) * vstride + hfo));
-        const int ts = min(t2, lim);
-        vm = Meta<MetaT>::load(vm_h + static_cast<size_t>(s0) * Hkv, static_cast<size_t>(ts * Hkv));
-        idv = in.ids[s0 + ts];
-        okv = t2 <= lim;
+        if (p == P - 1) {
+            fetch_at(p, off_last);
+            okv = t2 <= lim_last;
+        } else {
+            fetch_at(p, off_full);
+            okv = true;
+        }
     };
 
     // this wave's quarter of the workgroup's pairs
@@ -630,7 +676,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
             if (GP >= 4 || h < GP) {
                 *reinterpret_cast<mf_u4*>(bt + (h * kBRS + 8 * n) * 2) = hi;
                 *reinterpret_cast<mf_u4*>(bt + ((GP + h) * kBRS + 8 * n) * 2) = lo;
-                if (n == 0) bias_l[tile * 8 + h] = bp;
+                bias_l[tile * 8 + h] = bp;  // the 16 lanes of the row hold the same total
             }
         }
     };
@@ -732,9 +778,8 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
                 pv[tile][r] = e * vsv[tile][r];
             }
         l_run += lsum;
-        mf_u4 ahi, alo;
-        split_hl4(pv[0][0], pv[0][2], pv[0][1], pv[0][3], pv[1][0], pv[1][2], pv[1][1], pv[1][3], ahi, alo);
-        const mf_u4 ap = lo_col ? alo : ahi;
+        const mf_u4 ap = {split_half(pv[0][0], pv[0][2], negm_col), split_half(pv[0][1], pv[0][3], negm_col),
+                          split_half(pv[1][0], pv[1][2], negm_col), split_half(pv[1][1], pv[1][3], negm_col)};
 
         // B: codes of channel 4 beta + k for the lane's 8 tokens,
         // beta = n (nsteps 0..3) and n + 16 (nsteps 4..7), k = nstep & 3.
