@@ -788,13 +788,18 @@ const void* split_kernel_ptr(int gp, int fp16) {
     }
 }
 
-// Workgroups of the split launch the device holds at once: CUs x occupancy
+// CUs of the device and workgroups of the split launch one CU holds at once
 // (queried once per device and shape, then cached).
-int resident_split_wgs(int D, int G, int fp16) {
+struct Residency {
+    int cus = 256;
+    int per_cu = 2;
+};
+
+Residency split_residency(int D, int G, int fp16) {
     static std::mutex mu;
-    static std::map<std::tuple<int, int, int, int>, int> cache;
+    static std::map<std::tuple<int, int, int, int>, Residency> cache;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 1024;
+    if (hipGetDevice(&dev) != hipSuccess) return Residency{};
     const int gp = gp_for(G);
     const auto key = std::make_tuple(dev, D, gp, fp16);
     std::lock_guard<std::mutex> lock(mu);
@@ -818,7 +823,7 @@ int resident_split_wgs(int D, int G, int fp16) {
         (void)hipGetLastError();
         per_cu = 2;
     }
-    const int r = cus * per_cu;
+    const Residency r{cus, per_cu};
     cache[key] = r;
     return r;
 }
@@ -841,7 +846,8 @@ AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs,
     const int G = Hq / Hkv;
     const int chunks = (G + gp_for(G) - 1) / gp_for(G);
     const long long heads = static_cast<long long>(Hkv) * chunks;
-    const long long resident = resident_split_wgs(D, G, meta_fp16);
+    const Residency res = split_residency(D, G, meta_fp16);
+    const long long resident = static_cast<long long>(res.cus) * res.per_cu;
     const long long per_head = std::max<long long>(1, (resident + heads - 1) / heads);
     const long long dense_tiles = (dense_ub + 15) / 16;
     if (use_packed_kernel(D)) {
@@ -849,18 +855,35 @@ AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs,
         // each so the partials stay small (a 32-token pair of packed tiles is
         // one unit, a 16-token FP32 tile kDenseTileCost), shared between packed
         // and FP32 workgroups in proportion to their work.
-        constexpr long long kDenseTileCost = 2;
+        //
+        // When the launch fills the device, each kind gets whole dispatch
+        // rounds (one workgroup per CU each): the kernel's workgroup order
+        // sends slot groups of every head to the XCDs round-robin, so a round
+        // of `cus / heads` slots lands one workgroup on every CU, and every CU
+        // then runs the same mix of packed and FP32 work.
+        constexpr long long kDenseTileCost = 4;  // ~3.7x the bytes of a pair
         const long long pairs = (static_cast<long long>(blocks_ub) * W + 1) / 2;
         const long long dense_units = dense_tiles * kDenseTileCost;
         const long long units = pairs + dense_units;
-        const long long wgs = std::max<long long>(1, std::min(per_head, units / 8));
-        long long nd = 0;
-        if (dense_tiles > 0) {
-            nd = (wgs * dense_units + units / 2) / units;
-            nd = std::max<long long>(1, std::min(nd, dense_tiles));
+        const long long round = (res.cus % heads == 0) ? res.cus / heads : 0;  // slots per dispatch round
+        if (round > 0 && round % 8 == 0 && res.per_cu >= 2 && units / 8 >= round * res.per_cu) {
+            long long rd = 0;
+            if (dense_tiles > 0) {
+                rd = (res.per_cu * dense_units + units / 2) / units;
+                rd = std::max<long long>(1, std::min<long long>(rd, res.per_cu - 1));
+            }
+            p.nsplit_d = static_cast<int>(std::min(rd * round, dense_tiles));
+            p.nsplit_p = static_cast<int>((res.per_cu - rd) * round);
+        } else {
+            const long long wgs = std::max<long long>(1, std::min(per_head, units / 8));
+            long long nd = 0;
+            if (dense_tiles > 0) {
+                nd = (wgs * dense_units + units / 2) / units;
+                nd = std::max<long long>(1, std::min(nd, dense_tiles));
+            }
+            p.nsplit_d = static_cast<int>(nd);
+            p.nsplit_p = static_cast<int>(std::max<long long>(1, wgs - nd));
         }
-        p.nsplit_d = static_cast<int>(nd);
-        p.nsplit_p = static_cast<int>(std::max<long long>(1, wgs - nd));
     } else {
         // One round of resident workgroups, but at least ~32 packed-tile
         // units of work per workgroup so the merge traffic stays small.
