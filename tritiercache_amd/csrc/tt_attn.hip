@@ -604,6 +604,8 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int blk, float* sh) {
         }
     }
     // (M_h, 1/L_h) of every head: 8 threads per head, splits j0, j0 + 8, ...
+    // (every workgroup rebuilds them: a second launch that waits for the
+    // merge costs more than these loads)
     float* Mh = sh;        // [Hq]
     float* iL = sh + Hq;   // [Hq]
     for (int h0 = 0; h0 < Hq; h0 += 32) {

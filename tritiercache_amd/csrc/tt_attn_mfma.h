@@ -507,25 +507,28 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     const MetaT* ks_h = static_cast<const MetaT*>(in.ks) + kvh * kMfD;
     const MetaT* kz_h = static_cast<const MetaT*>(in.kz) + kvh * kMfD;
     const int32_t* vp_h = in.vp + kvh * (kMfD / 16);
-    const MetaT* vm_h = static_cast<const MetaT*>(lane < 32 ? in.vs : in.vz) + kvh;
+    const MetaT* vs_h = static_cast<const MetaT*>(in.vs) + kvh;
+    const MetaT* vz_h = static_cast<const MetaT*>(in.vz) + kvh;
     const int lk = 4 * (lane & 31);
     const int tv = 4 * (lane >> 3) + (lane & 3);
     const int hfo = 4 * ((lane >> 2) & 1);
     const int t2 = lane & 31;
 
-    // Per-lane element offsets of a pair's loads from the pair's base
-    // addresses: those of a whole pair, and those of the store's last pair,
-    // which may hold one tile (kto = 0 for both halves) and fewer slots
-    // (lanes past the end re-read the last slot and are masked).
+    // Per-lane byte offsets of a pair's loads from the pair's (wave-uniform)
+    // base addresses, so the loads take a scalar base and a 32-bit lane
+    // offset: those of a whole pair, and those of the store's last pair, which
+    // may hold one tile (kto = 0 for both halves) and fewer slots (lanes past
+    // the end re-read the last slot and are masked).
     struct PairOffs {
         uint32_t k, km, v, vm, id;
     };
     auto pair_offs = [&](const int kto, const int lim) {
         const int ts = min(t2, lim);
-        return PairOffs{static_cast<uint32_t>(kto * tstride + lk),
-                        static_cast<uint32_t>(((W == 2) ? 0 : kto) * tstride + lk),
-                        static_cast<uint32_t>(min(tv, lim) * vstride + hfo), static_cast<uint32_t>(ts * Hkv),
-                        static_cast<uint32_t>(ts)};
+        return PairOffs{static_cast<uint32_t>(kto * tstride + lk) * 4u,
+                        static_cast<uint32_t>(((W == 2) ? 0 : kto) * tstride + lk) * static_cast<uint32_t>(sizeof(MetaT)),
+                        static_cast<uint32_t>(min(tv, lim) * vstride + hfo) * 4u,
+                        static_cast<uint32_t>(ts * Hkv) * static_cast<uint32_t>(sizeof(MetaT)),
+                        static_cast<uint32_t>(ts) * 8u};
     };
     const PairOffs off_full = pair_offs(lane >> 5, 31);
     const int lim_last = nslots - 1 - 32 * (P - 1);
@@ -539,16 +542,21 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     bool okv = false;
 
     // Wave-uniform bases (scalar) plus the per-lane offsets.
+    auto at = [](const void* base, const uint32_t off) { return static_cast<const char*>(base) + off; };
     auto fetch_at = [&](const int p, const PairOffs& o) {
         const size_t kb = static_cast<size_t>(2 * p) * tstride;
         const size_t mb = static_cast<size_t>((W == 2) ? p : 2 * p) * tstride;
         const size_t s0 = static_cast<size_t>(32 * p);
-        kw = *reinterpret_cast<const mf_u4*>(kp_h + kb + o.k);
-        ksr = load_meta4<MetaT>(ks_h + mb + o.km);
-        kzr = load_meta4<MetaT>(kz_h + mb + o.km);
-        vw = *reinterpret_cast<const mf_u4*>(vp_h + s0 * vstride + o.v);
-        vm = Meta<MetaT>::load(vm_h + s0 * Hkv, o.vm);
-        idv = in.ids[s0 + o.id];
+        kw = *reinterpret_cast<const mf_u4*>(at(kp_h + kb, o.k));
+        ksr = load_meta4<MetaT>(reinterpret_cast<const MetaT*>(at(ks_h + mb, o.km)));
+        kzr = load_meta4<MetaT>(reinterpret_cast<const MetaT*>(at(kz_h + mb, o.km)));
+        vw = *reinterpret_cast<const mf_u4*>(at(vp_h + s0 * vstride, o.v));
+        // V scale in lanes 0-31, V zero in lanes 32-63 (two half-wave loads)
+        if (lane < 32)
+            vm = Meta<MetaT>::load(reinterpret_cast<const MetaT*>(at(vs_h + s0 * Hkv, o.vm)), 0);
+        else
+            vm = Meta<MetaT>::load(reinterpret_cast<const MetaT*>(at(vz_h + s0 * Hkv, o.vm)), 0);
+        idv = *reinterpret_cast<const long long*>(at(in.ids + s0, o.id));
     };
     auto fetch = [&](const int p) {
         if (p == P - 1) {
