@@ -12,9 +12,13 @@ every step streams from HBM, not from the 256 MB Infinity Cache.
 
 One step = for each of the 32 layers, tt_fused_attention_decode_ws (split-K
 partials, log-sum-exp merge, mean attention weights), replayed as one HIP graph.
-The dominant kernel (attn_tiles_kernel: split-K partials over the FP32 tiles
-and, on the matrix cores, the packed blocks) is also timed on its own with HIP
-events on the launch stream, for the roofline.
+The dominant kernel (attn_packed_kernel: split-K partials, the packed blocks on
+the matrix cores and the FP32 tiers on the VALU) is also timed on its own: a
+HIP graph of the 32 layers' partials launches, HIP events on the launch
+stream, time / 32 per launch (the figure rocprofv3 reports as the kernel's
+average duration). `traffic` is the kernel's HBM bytes per launch from
+rocprofv3 counters, read from the committed counter summary under profiles/
+(made with --pmc-driver and --pmc-summary, see there).
 
 The CPU baseline is the reference's own AVX2+OpenMP kernel
 (oracle/_ref/libttref.so, compiled from the reference sources) on the host
@@ -119,6 +123,100 @@ def build_layers(torch, L, Hq, Hkv, D, ctx, layers, outliers, seed):
     return out, (nd, npk, nb)
 
 
+PMC_TRAFFIC_MD = os.path.join(ROOT, "profiles", "attn_packed_kernel_llama3-8b-32k_hbm_traffic.md")
+
+
+def traffic_from_profile(config, meta):
+    """HBM bytes per partials launch (reads + writes) from the committed counter summary, when it covers this
+    workload and metadata type; None otherwise."""
+    if config != "llama3-8b-32k" or not os.path.exists(PMC_TRAFFIC_MD):
+        return None
+    for line in open(PMC_TRAFFIC_MD):
+        if line.startswith(f"traffic_bytes_per_launch[{meta}]:"):
+            return int(line.split(":")[1])
+    return None
+
+
+def pmc_driver(torch, lib, L, data, layer_args, tag, fp16, ws, ws_bytes, sp):
+    """Workload for rocprofv3 --pmc: the calibration copy, then 5 partials launches of layer 0 with cache
+    eviction in between (so every launch reads its layer from HBM)."""
+    src = torch.empty(64 << 20, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    d = data[0]
+    for _ in range(5):
+        L.check(lib.tt_attention_partials(*layer_args(d, tag), 16, fp16, 1, ws.data_ptr(), ws_bytes, sp()),
+                "partials")
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("[bench] pmc driver done", file=sys.stderr)
+
+
+def pmc_summary(dirs):
+    """Markdown summary of rocprofv3 --pmc runs of --pmc-driver: per-dispatch counter values of the partials
+    kernel and of the 256 MiB copy (calibration), and the HBM bytes per launch they give."""
+    import collections
+    import csv
+    import glob
+
+    vals = collections.defaultdict(list)  # (kernel, counter) -> per-dispatch totals
+    for d in dirs:
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            per = collections.defaultdict(float)
+            names = {}
+            for r in csv.DictReader(open(f)):
+                k = r["Kernel_Name"]
+                kind = ("attn_packed_kernel<4, float>" if "attn_packed_kernel<4, float>" in k else
+                        "attn_packed_kernel<4, unsigned short>" if "attn_packed_kernel<4, unsigned short>" in k else
+                        "copy 256 MiB (calibration)" if "copyBuffer" in k else None)
+                if kind is None:
+                    continue
+                per[(r["Dispatch_Id"], r["Counter_Name"])] += float(r["Counter_Value"])
+                names[r["Dispatch_Id"]] = kind
+            for (did, c), v in per.items():
+                vals[(names[did], c)].append(v)
+    med = {k: sorted(v)[len(v) // 2] for k, v in vals.items()}
+    print("| dispatch | counter | per dispatch (median) | dispatches |")
+    print("|:--|:--|--:|--:|")
+    for (k, c), v in sorted(vals.items()):
+        print(f"| {k} | {c} | {med[(k, c)]:.0f} | {len(v)} |")
+    copy = "copy 256 MiB (calibration)"
+    fs, ws_ = med.get((copy, "FETCH_SIZE")), med.get((copy, "WRITE_SIZE"))
+    if not fs or not ws_:
+        return
+    ff, wf = 262144.0 / fs, 262144.0 / ws_
+    print(f"\ncalibration: the copy reads and writes 262144 KiB; FETCH_SIZE reads {fs:.0f} KiB (factor {ff:.3f}), "
+          f"WRITE_SIZE {ws_:.0f} KiB (factor {wf:.3f})\n")
+    for k, meta in (("attn_packed_kernel<4, float>", "fp32"), ("attn_packed_kernel<4, unsigned short>", "fp16")):
+        if (k, "FETCH_SIZE") in med and (k, "WRITE_SIZE") in med:
+            rd = med[(k, "FETCH_SIZE")] * ff * 1024
+            wr = med[(k, "WRITE_SIZE")] * wf * 1024
+            print(f"{k}: reads {rd / 1e6:.2f} MB, writes {wr / 1e6:.2f} MB per launch\n")
+            print(f"traffic_bytes_per_launch[{meta}]: {int(rd + wr)}\n")
+
+
+def trace_summary(db_path):
+    """Markdown table of kernel durations (calls, average, median, min, max, share of GPU time) from a
+    rocprofv3 --kernel-trace results database."""
+    import collections
+    import sqlite3
+
+    rows = sqlite3.connect(db_path).execute("select name, start, end from kernels").fetchall()
+    dur = collections.defaultdict(list)
+    for name, s, e in rows:
+        n = name.replace("(anonymous namespace)::", "").replace("void ", "")
+        dur[n.split("(")[0]].append((e - s) / 1e3)
+    total = sum(sum(v) for v in dur.values())
+    print("| kernel | calls | avg (us) | median (us) | min (us) | max (us) | % of GPU time |")
+    print("|:--|--:|--:|--:|--:|--:|--:|")
+    for k, v in sorted(dur.items(), key=lambda kv: -sum(kv[1]))[:8]:
+        v.sort()
+        print(f"| `{k[:70]}` | {len(v)} | {sum(v) / len(v):.2f} | {v[len(v) // 2]:.2f} | {v[0]:.2f} | {v[-1]:.2f} | "
+              f"{100.0 * sum(v) / total:.1f} |")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -130,7 +228,20 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true", help="launch layers directly instead of a HIP graph")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--pmc-driver", action="store_true",
+                    help="counter-run workload: a 256 MiB device copy (calibration), then the partials kernel of one "
+                         "layer 5 times, each after a 256 MiB copy that evicts the caches; run under rocprofv3 --pmc")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="DIR",
+                    help="print the markdown counter summary of rocprofv3 --pmc output directories")
+    ap.add_argument("--trace-summary", metavar="DB",
+                    help="print the markdown kernel table of a rocprofv3 --kernel-trace results database")
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
+    if args.trace_summary:
+        trace_summary(args.trace_summary)
+        return
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -147,7 +258,7 @@ def main():
     torch.cuda.set_device(0)
     Hq, Hkv, D, ctx, layers, outl = CONFIGS[args.config]
     t0 = time.time()
-    data, (nd, npk, nb) = build_layers(torch, L, Hq, Hkv, D, ctx, layers, outl, args.seed)
+    data, (nd, npk, nb) = build_layers(torch, L, Hq, Hkv, D, ctx, 1 if args.pmc_driver else layers, outl, args.seed)
     print(f"[bench] built {layers} layers ({nd} dense + {nb} blocks each) in {time.time() - t0:.1f}s", file=sys.stderr,
           flush=True)
 
@@ -194,22 +305,36 @@ def main():
         return e0.elapsed_time(e1) * 1000.0 / args.steps, g is not None
 
     def time_split_kernel(t, f16, reps):
-        """Average duration of one attn_tiles_kernel launch (HIP events on the launch stream)."""
-        evs = []
-        for _ in range(reps):
+        """Average duration of one attn_packed_kernel launch: the 32 layers' partials launches back to back
+        (one HIP graph), HIP events on the launch stream around `reps` replays."""
+        def partials():
             for d in data:
-                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-                a.record()
                 L.check(lib.tt_attention_partials(*layer_args(d, t), 16, f16, 1, ws.data_ptr(), ws_bytes, sp()),
                         "partials")
-                b.record()
-                L.check(lib.tt_attention_finalize(d["Q"].data_ptr(), nd, nb, Hq, Hkv, D, d["out"].data_ptr(),
-                                                  d["mw"].data_ptr(), 16, f16, 1, ws.data_ptr(), ws_bytes, sp()),
-                        "finalize")
-                evs.append((a, b))
+        run = partials
+        if not args.no_graph:
+            try:
+                partials()
+                torch.cuda.synchronize()
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g):
+                    partials()
+                run = g.replay
+            except Exception as e:  # pragma: no cover
+                print(f"[bench] graph capture of the partials failed ({e}); timing direct launches", file=sys.stderr)
+        run()
         torch.cuda.synchronize()
-        ms = [a.elapsed_time(b) for a, b in evs]
-        return 1000.0 * sum(ms) / len(ms)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1000.0 / (reps * len(data))
+
+    if args.pmc_driver:
+        pmc_driver(torch, lib, L, data, layer_args, tag, fp16, ws, ws_bytes, sp)
+        return
 
     us_step, graphed = time_steps(tag, fp16)
     other_tag, other_fp16 = ("16", 1) if not fp16 else ("32", 0)
@@ -290,12 +415,12 @@ def main():
         "bytes_read_per_step": bpl * layers,
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_tiles_kernel",
+            "kernel": "attn_packed_kernel",
             "achieved": round(kern_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(kern_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic_from_profile(args.config, args.meta),
             "bytes_per_launch": bpl,
             "avg_launch_us": round(split_us, 3),
         },
