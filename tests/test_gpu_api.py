@@ -1,0 +1,353 @@
+"""Python API and HF patch on the GPU, mirroring the reference's own tests:
+tests/test_cache_init.py (TriTierCache construction), tests/test_wiring_verification.py
+(k_group_size / metadata-dtype wiring through _C), tests/test_patch_llama.py and
+tests/test_multi_model_patch.py (the attention patch on tiny offline configs).
+Here every module and tensor lives on the ROCm device and the engine runs on it;
+decode outputs are also checked against float32 attention over the engine's own
+reconstructed tiers.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    assert torch.cuda.is_available(), "GPU test on a machine without a GPU"
+
+
+# ---------------------------------------------------------------------------
+# TriTierCache construction (reference tests/test_cache_init.py)
+# ---------------------------------------------------------------------------
+MAX_SEQ_LEN, HEAD_DIM, NUM_HEADS, R_SIZE, H_RATIO = 128, 16, 4, 32, 0.05
+
+
+@pytest.fixture
+def cache():
+    from tritiercache_amd.cache import TriTierCache
+
+    return TriTierCache(max_seq_len=MAX_SEQ_LEN, head_dim=HEAD_DIM, num_heads=NUM_HEADS, R_size=R_SIZE,
+                        H_ratio=H_RATIO)
+
+
+def test_cache_constructs_on_the_engine(cache):
+    assert cache._engine is not None
+    assert cache.RW_K_Buffer.device.type == "cuda"
+
+
+def test_cache_sizing(cache):
+    from tritiercache_amd.constants import CHUNK_SIZE
+
+    assert cache.R_size + cache.max_heavy_hitters + cache.max_background_tokens == MAX_SEQ_LEN
+    assert cache.num_blocks == math.ceil(cache.max_background_tokens / CHUNK_SIZE)
+    assert cache.quant_head_dim == math.ceil(HEAD_DIM / 16)
+
+
+def test_cache_tier_buffers(cache):
+    from tritiercache_amd.constants import CHUNK_SIZE
+
+    assert cache.RW_K_Buffer.shape == (R_SIZE, NUM_HEADS, HEAD_DIM)
+    assert cache.RW_V_Buffer.shape == (R_SIZE, NUM_HEADS, HEAD_DIM)
+    assert cache.RW_K_Buffer.dtype == torch.float32
+    assert cache.RW_count == 0 and cache.RW_head_index == 0
+    n = cache.max_heavy_hitters
+    assert cache.HH_K_Buffer.shape == (n, NUM_HEADS, HEAD_DIM)
+    assert cache.HH_token_ids.shape == (n,) and cache.HH_token_ids.dtype == torch.int64
+    assert cache.HH_scores.shape == (n,) and cache.HH_scores.dtype == torch.float32
+    assert torch.all(cache.HH_token_ids == -1)
+    assert cache.HH_count == 0
+    assert cache.WR_K_Buffer.shape == (CHUNK_SIZE, NUM_HEADS, HEAD_DIM)
+    assert cache.WR_token_ids.shape == (CHUNK_SIZE,)
+    assert torch.all(cache.WR_token_ids == -1)
+    assert cache.WR_count == 0
+    assert cache.Global_Attn_Scr.shape == (MAX_SEQ_LEN,)
+    assert torch.all(cache.Global_Attn_Scr == 0.0)
+    assert cache.current_threshold == 0.0
+    assert cache.PBS_count == 0
+
+
+def test_cache_counters_are_read_only_with_the_engine(cache):
+    with pytest.raises(AttributeError):
+        cache.Total_Processed_Tokens = 3
+
+
+# ---------------------------------------------------------------------------
+# _C wiring (reference tests/test_wiring_verification.py)
+# ---------------------------------------------------------------------------
+def test_k_group_size_wiring():
+    from tritiercache_amd import _C
+
+    H, D, T = 4, 64, 32
+    rng = np.random.default_rng(42)
+    K = np.zeros((T, H, D), np.float32)
+    K[:16] = rng.uniform(-1.0, 1.0, (16, H, D))
+    K[16:] = rng.uniform(5.0, 10.0, (16, H, D))
+    p16 = np.zeros((2, H, D), np.int32)
+    s16 = np.zeros((2, H, D), np.float32)
+    z16 = np.zeros((2, H, D), np.float32)
+    _C.quantize_k_block(K[:16], p16[0], s16[0], z16[0], H, D, 16, "fp32")
+    _C.quantize_k_block(K[16:], p16[1], s16[1], z16[1], H, D, 16, "fp32")
+    d16 = np.zeros((T, H, D), np.float32)
+    _C.dequantize_k(p16, s16, z16, d16, 2, H, D, 16, "fp32")
+    p32 = np.zeros((2, H, D), np.int32)
+    s32 = np.zeros((1, H, D), np.float32)
+    z32 = np.zeros((1, H, D), np.float32)
+    _C.quantize_k_block(K, p32, s32, z32, H, D, 32, "fp32")
+    d32 = np.zeros((T, H, D), np.float32)
+    _C.dequantize_k(p32, s32, z32, d32, 1, H, D, 32, "fp32")
+    assert not np.array_equal(p16, p32)
+    assert np.max(np.abs(d16 - d32)) > 0.1
+    # each block size reconstructs its own tokens within half a step
+    assert np.all(np.abs(d16[:16] - K[:16]) <= s16[0] * 0.5 + 1e-6)
+    assert np.all(np.abs(d32 - K) <= s32 * 0.5 + 1e-5)
+
+
+def test_pbs_metadata_dtype_wiring():
+    from tritiercache_amd import _C
+
+    H, D, T = 4, 64, 16
+    K = (np.random.default_rng(42).standard_normal((T, H, D)) * 2.5 + 1.2345).astype(np.float32)
+    out = {}
+    for meta, mdt in (("fp32", np.float32), ("fp16", np.uint16)):
+        p = np.zeros((1, H, D), np.int32)
+        s = np.zeros((1, H, D), mdt)
+        z = np.zeros((1, H, D), mdt)
+        _C.quantize_k_block(K, p, s, z, H, D, 16, meta)
+        d = np.zeros((T, H, D), np.float32)
+        _C.dequantize_k(p, s, z, d, 1, H, D, 16, meta)
+        out[meta] = (s, d)
+    assert out["fp16"][0].itemsize == 2 and out["fp32"][0].itemsize == 4
+    diff = np.max(np.abs(out["fp32"][1] - out["fp16"][1]))
+    assert 0 < diff < 0.05
+
+
+def _engines():
+    from tritiercache_amd import _C
+
+    args = (4, 2, 64, 256, 4, 16, 0.1, 0.999, 16)
+    return {"16/fp16": _C.TriTierCacheEngine(*args, 16, "fp16"), "16/fp32": _C.TriTierCacheEngine(*args, 16, "fp32"),
+            "32/fp16": _C.TriTierCacheEngine(*args, 32, "fp16")}
+
+
+def test_engine_properties_and_memory_sensitivity():
+    eng = _engines()
+    assert eng["16/fp16"].k_group_size == 16 and eng["16/fp16"].pbs_metadata_dtype == "fp16"
+    assert eng["16/fp16"].use_fp16_meta is True
+    assert eng["16/fp32"].use_fp16_meta is False and eng["16/fp32"].pbs_metadata_dtype == "fp32"
+    assert eng["32/fp16"].k_group_size == 32
+    rng = np.random.default_rng(123)
+    Kp = rng.standard_normal((96, 2, 64)).astype(np.float32)
+    Vp = rng.standard_normal((96, 2, 64)).astype(np.float32)
+    for e in eng.values():
+        e.prefill(Kp, Vp, 96)
+        assert e.pbs_count > 0
+    assert eng["16/fp16"].get_buffer_bytes() < eng["16/fp32"].get_buffer_bytes()
+
+
+def test_engine_attention_step_differs_across_configurations():
+    eng = _engines()
+    rng = np.random.default_rng(999)
+    Kp = rng.standard_normal((96, 2, 64)).astype(np.float32)
+    Vp = rng.standard_normal((96, 2, 64)).astype(np.float32)
+    Q = rng.standard_normal(4 * 64).astype(np.float32)
+    Kn = rng.standard_normal(2 * 64).astype(np.float32)
+    Vn = rng.standard_normal(2 * 64).astype(np.float32)
+    outs = {}
+    for k, e in eng.items():
+        e.prefill(Kp, Vp, 96)
+        o = np.zeros(4 * 64, np.float32)
+        e.step(Q, Kn, Vn, o)
+        assert np.all(np.isfinite(o)) and np.any(o != 0.0)
+        outs[k] = o
+    assert np.max(np.abs(outs["16/fp16"] - outs["32/fp16"])) > 0
+    assert np.max(np.abs(outs["16/fp16"] - outs["16/fp32"])) > 0
+
+
+# ---------------------------------------------------------------------------
+# Engine decode against float32 attention over the reconstructed tiers
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("Hq,Hkv,D,kgs,meta", [(8, 2, 128, 16, "fp16"), (8, 8, 64, 32, "fp32"),
+                                               (12, 4, 128, 32, "fp32")])
+def test_decode_matches_attention_over_reconstructed_cache(Hq, Hkv, D, kgs, meta):
+    from tritiercache_amd.cache import TriTierCache
+
+    torch.manual_seed(Hq * 1000 + D + kgs)
+    c = TriTierCache(max_seq_len=1024, head_dim=D, num_heads=Hkv, R_size=64, H_ratio=0.05, num_q_heads=Hq,
+                     k_group_size=kgs, pbs_metadata_dtype=meta)
+    c.prefill(torch.randn(300, Hkv, D, device=DEV), torch.randn(300, Hkv, D, device=DEV))
+    out = torch.empty(Hq * D, device=DEV)
+    for step in range(40):  # past ring overflow, routing and at least one waiting-room flush
+        Q = torch.randn(Hq * D, device=DEV)
+        Kn, Vn = torch.randn(Hkv * D, device=DEV), torch.randn(Hkv * D, device=DEV)
+        c.step(Q, Kn, Vn, out)
+        Kf, Vf, ids = c.reconstruct_full_cache()
+        assert Kf.shape[0] == c.Total_Processed_Tokens - c.WR_count
+        rep = Hq // Hkv
+        Kh = Kf.permute(1, 0, 2).repeat_interleave(rep, dim=0)  # [Hq, N, D]
+        Vh = Vf.permute(1, 0, 2).repeat_interleave(rep, dim=0)
+        q = Q.view(Hq, 1, D)
+        w = torch.softmax(torch.matmul(q, Kh.transpose(1, 2).contiguous()) / math.sqrt(D), dim=-1)
+        ref = torch.matmul(w, Vh).reshape(-1)
+        err = (out - ref).abs().max() / ref.abs().max()
+        assert err <= 1e-4, (step, float(err))
+    assert c.PBS_count > 300 - 4 - 64 - c.max_heavy_hitters - kgs
+
+
+# ---------------------------------------------------------------------------
+# HF patch (reference tests/test_patch_llama.py, tests/test_multi_model_patch.py)
+# ---------------------------------------------------------------------------
+transformers = pytest.importorskip("transformers")
+
+
+@pytest.fixture
+def patched():
+    from tritiercache_amd.integration import patch_model
+
+    patch_model.apply_patch()
+    yield patch_model
+    patch_model.remove_patch()
+
+
+def _llama_attention(num_q_heads=4, num_kv_heads=4, hidden_size=64, head_dim=16):
+    from transformers.models.llama.configuration_llama import LlamaConfig
+    from transformers.models.llama.modeling_llama import LlamaAttention, LlamaRotaryEmbedding
+
+    cfg = LlamaConfig(hidden_size=hidden_size, num_attention_heads=num_q_heads, num_key_value_heads=num_kv_heads,
+                      head_dim=head_dim, max_position_embeddings=4096, attention_bias=False)
+    return LlamaAttention(cfg, layer_idx=0).to(DEV), LlamaRotaryEmbedding(config=cfg).to(DEV), cfg
+
+
+def _pos(rotary, h, positions):
+    return rotary(h, torch.tensor([positions], device=DEV))
+
+
+def test_patch_replaces_and_restores_forwards(patched):
+    from transformers.models.llama.modeling_llama import LlamaAttention
+    from transformers.models.mistral.modeling_mistral import MistralAttention
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention
+
+    assert patched.is_patched()
+    for cls in (LlamaAttention, MistralAttention, Qwen2Attention):
+        assert cls.forward == patched.patched_forward
+    patched.remove_patch()
+    assert not patched.is_patched()
+    for cls in (LlamaAttention, MistralAttention, Qwen2Attention):
+        assert cls.forward != patched.patched_forward
+    patched.apply_patch()
+
+
+def test_batch_size_above_one_is_rejected(patched):
+    layer, rot, cfg = _llama_attention()
+    h = torch.randn(2, 1, cfg.hidden_size, device=DEV)
+    cos, sin = rot(h, torch.tensor([[0], [0]], device=DEV))
+    with pytest.raises(AssertionError, match="TriTierCache only supports batch_size=1"):
+        layer(h, position_embeddings=(cos, sin))
+
+
+def test_prefill_then_decode_creates_engine_cache(patched):
+    from tritiercache_amd.cache import TriTierCache
+
+    layer, rot, cfg = _llama_attention(num_q_heads=4, num_kv_heads=2)
+    assert not hasattr(layer, "tri_tier_cache")
+    h = torch.randn(1, 4, cfg.hidden_size, device=DEV)
+    out, w = layer(h, position_embeddings=_pos(rot, h, [0, 1, 2, 3]))
+    assert out.shape == (1, 4, cfg.hidden_size) and not torch.isnan(out).any()
+    c = layer.tri_tier_cache
+    assert isinstance(c, TriTierCache) and c._engine is not None
+    assert c.num_heads == cfg.num_key_value_heads and c.head_dim == 16 and c.R_size == patched.R_SIZE
+    assert c.Total_Processed_Tokens == 4
+    h1 = torch.randn(1, 1, cfg.hidden_size, device=DEV)
+    out, w = layer(h1, position_embeddings=_pos(rot, h1, [4]))
+    assert out.shape == (1, 1, cfg.hidden_size) and out.device.type == "cuda" and w is None
+    assert c.Total_Processed_Tokens == 5
+
+
+@pytest.mark.parametrize("nq,nkv,hid,hd", [(4, 4, 64, 16), (8, 2, 128, 16)])
+def test_decode_with_attention_weights(patched, nq, nkv, hid, hd):
+    layer, rot, cfg = _llama_attention(nq, nkv, hid, hd)
+    h = torch.randn(1, 1, hid, device=DEV)
+    out, w = layer(h, position_embeddings=_pos(rot, h, [0]))
+    assert out.shape == (1, 1, hid) and w is None
+    h = torch.randn(1, 1, hid, device=DEV)
+    out, w = layer(h, position_embeddings=_pos(rot, h, [1]), output_attentions=True)
+    assert out.shape == (1, 1, hid) and not torch.isnan(out).any()
+    assert w.shape == (1, nq, 1, 2)
+    assert torch.allclose(w.float().sum(dim=-1), torch.ones(1, nq, 1, device=DEV), atol=1e-5)
+
+
+def test_multi_step_decode_across_eviction_and_quantization(patched):
+    from tritiercache_amd.constants import CHUNK_SIZE, SINK_SIZE
+
+    layer, rot, cfg = _llama_attention(4, 4, 64, 16)
+    steps = SINK_SIZE + patched.R_SIZE + CHUNK_SIZE + 10
+    for s in range(steps):
+        h = torch.randn(1, 1, 64, device=DEV)
+        out, w = layer(h, position_embeddings=_pos(rot, h, [s]), output_attentions=True)
+        assert out.shape == (1, 1, 64) and torch.isfinite(out).all()
+        c = layer.tri_tier_cache
+        assert w.shape == (1, 4, 1, (s + 1) - c.WR_count)
+        assert torch.allclose(w.float().sum(dim=-1), torch.ones(1, 4, 1, device=DEV), atol=1e-4)
+    c = layer.tri_tier_cache
+    assert c.Total_Processed_Tokens == steps and c.S_count == SINK_SIZE and c.RW_count == patched.R_SIZE
+    assert c.PBS_count >= CHUNK_SIZE or c.HH_count > 0
+
+
+def test_end_to_end_causal_lm_generate(patched):
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(vocab_size=100, hidden_size=64, intermediate_size=128, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=16, max_position_embeddings=256,
+                      pad_token_id=0, bos_token_id=1, eos_token_id=2)
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).to(DEV).eval()
+    with torch.no_grad():
+        out = model.generate(torch.tensor([[1]], device=DEV), max_new_tokens=15, use_cache=True, eos_token_id=None,
+                             do_sample=False)
+    assert out.shape == (1, 16)
+    c0 = model.model.layers[0].self_attn.tri_tier_cache
+    c1 = model.model.layers[1].self_attn.tri_tier_cache
+    assert c0 is not c1
+    assert c0.Total_Processed_Tokens == 15 and c1.Total_Processed_Tokens == 15
+    assert float(c0.Global_Attn_Scr[:15].sum()) > 0
+    patched.reset_caches(model)
+    assert not hasattr(model.model.layers[0].self_attn, "tri_tier_cache")
+
+
+@pytest.mark.parametrize("arch", ["mistral", "qwen2", "qwen3"])
+def test_other_architectures_prefill_and_decode(patched, arch):
+    import transformers as tf
+
+    if arch == "mistral":
+        cfg = tf.MistralConfig(hidden_size=256, num_attention_heads=8, num_key_value_heads=4, head_dim=64)
+        from transformers.models.mistral.modeling_mistral import MistralAttention as A
+        q_len = 32
+    elif arch == "qwen2":
+        cfg = tf.Qwen2Config(hidden_size=512, num_attention_heads=4, num_key_value_heads=2, head_dim=128)
+        from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention as A
+        q_len = 20
+    else:
+        if not hasattr(tf, "Qwen3Config"):
+            pytest.skip("Qwen3 not in the installed transformers")
+        cfg = tf.Qwen3Config(hidden_size=256, num_attention_heads=4, num_key_value_heads=2, head_dim=64)
+        from transformers.models.qwen3.modeling_qwen3 import Qwen3Attention as A
+        q_len = 24
+    layer = A(cfg, layer_idx=0).to(DEV)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    h = torch.randn(1, q_len, cfg.hidden_size, device=DEV, generator=g)
+    cos = torch.randn(1, q_len, cfg.head_dim, device=DEV, generator=g)
+    sin = torch.randn(1, q_len, cfg.head_dim, device=DEV, generator=g)
+    out, _ = layer(h, position_embeddings=(cos, sin))
+    assert out.shape == (1, q_len, cfg.hidden_size)
+    assert layer.tri_tier_cache.head_dim == cfg.head_dim
+    assert layer.tri_tier_cache.Total_Processed_Tokens == q_len
+    ht = torch.randn(1, 1, cfg.hidden_size, device=DEV, generator=g)
+    out, _ = layer(ht, position_embeddings=(torch.randn(1, 1, cfg.head_dim, device=DEV, generator=g),
+                                            torch.randn(1, 1, cfg.head_dim, device=DEV, generator=g)))
+    assert out.shape == (1, 1, cfg.hidden_size) and torch.isfinite(out).all()
+    assert layer.tri_tier_cache.Total_Processed_Tokens == q_len + 1

@@ -394,7 +394,9 @@ class TriTierCacheEngine:
         k = st.ptr(k_ptr, "K_new", Hkv * D * 4)
         v = st.ptr(v_ptr, "V_new", Hkv * D * 4)
         o = st.ptr(out_ptr, "attn_output", Hq * D * 4, writable=True)
-        cap = self.visible() + 1
+        # the step adds the new token, and a waiting-room flush makes up to
+        # one more chunk of tokens visible
+        cap = self.visible() + 1 + self._chunk_size
         w = torch.empty((Hq, cap), dtype=torch.float32, device="cuda")
         vis = C.c_int(0)
         _lib.check(_L.tt_engine_step_weights(self._h, q, k, v, o, w.data_ptr(), cap, C.byref(vis), _stream()),

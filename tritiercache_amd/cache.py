@@ -342,7 +342,11 @@ class TriTierCache:
 
     def reconstruct_full_cache(self):
         """Dequantised view of every attended token: sinks, heavy hitters and
-        valid packed tokens sorted by id, then the recent window oldest first."""
+        valid packed tokens sorted by id, then the recent window oldest first
+        (cache.py:326-372 of the reference). With the device engine the tiers
+        are read from the engine (either block size, either metadata type)."""
+        if self._engine is not None:
+            return self._reconstruct_engine()
         dev = self.S_K_Buffer.device
         sk = self.S_K_Buffer[0:self.S_count]
         sv = self.S_V_Buffer[0:self.S_count]
@@ -378,6 +382,56 @@ class TriTierCache:
 
         return (torch.cat([sk, mk, rk], dim=0), torch.cat([sv, mv, rv], dim=0),
                 torch.cat([sids, mids, rids], dim=0))
+
+
+def _meta_f32(t: torch.Tensor) -> torch.Tensor:
+    """Scale / zero metadata as f32 (FP16 metadata is kept as uint16 bits)."""
+    return t.view(torch.float16).float() if t.dtype == torch.uint16 else t
+
+
+def _reconstruct_engine(self):
+    """reconstruct_full_cache() over the engine's device tiers."""
+    e = self._engine
+    c = e.counters()
+    s, hh, rw, nb = c["s_count"], c["hh_count"], c["rw_count"], c["pbs_blocks_used"]
+    total, head = c["total_processed_tokens"], c["rw_head_index"]
+    H, D, kgs = self.num_heads, self.head_dim, e.k_group_size
+    sk, sv = e.get_S_K()[:s], e.get_S_V()[:s]
+    dev = sk.device
+    sids = torch.arange(0, s, device=dev, dtype=torch.int64)
+
+    # K words: [block][kgs / 16][H][D], token 16 w + t of a block at bits 2t of word w
+    kp = e.get_PBS_K_Packed()[:nb]
+    tshift = torch.arange(0, 32, 2, dtype=torch.int32, device=dev).view(1, 1, 16, 1, 1)
+    kq = torch.bitwise_and(torch.bitwise_right_shift(kp.unsqueeze(2), tshift), 0b11).reshape(nb * kgs, H, D)
+    t3k = (kq.float() * _meta_f32(e.get_PBS_K_Scales()[:nb]).repeat_interleave(kgs, dim=0)
+           + _meta_f32(e.get_PBS_K_Zeroes()[:nb]).repeat_interleave(kgs, dim=0))
+    # V words: [slot][H][D / 16], channel 16 g + i at bits 2i of word g
+    vp = e.get_PBS_V_Packed()[: nb * kgs]
+    cshift = torch.arange(0, 32, 2, dtype=torch.int32, device=dev)
+    vq = torch.bitwise_and(torch.bitwise_right_shift(vp.unsqueeze(-1), cshift), 0b11).reshape(nb * kgs, H, -1)[..., :D]
+    t3v = vq.float() * _meta_f32(e.get_PBS_V_Scales()[: nb * kgs]) + _meta_f32(e.get_PBS_V_Zeroes()[: nb * kgs])
+    pids = e.get_PBS_token_ids()[: nb * kgs]
+    keep = pids != -1
+    mk = torch.cat([e.get_HH_K()[:hh], t3k[keep]], dim=0)
+    mv = torch.cat([e.get_HH_V()[:hh], t3v[keep]], dim=0)
+    mids = torch.cat([e.get_HH_token_ids()[:hh], pids[keep]], dim=0)
+    if mids.numel() > 0:
+        perm = torch.argsort(mids)
+        mk, mv, mids = mk[perm], mv[perm], mids[perm]
+
+    R = self.R_size
+    if rw < R:
+        rk, rv = e.get_RW_K()[:rw], e.get_RW_V()[:rw]
+        rids = torch.arange(s, s + rw, device=dev, dtype=torch.int64)
+    else:
+        rk = torch.roll(e.get_RW_K(), shifts=-head, dims=0)
+        rv = torch.roll(e.get_RW_V(), shifts=-head, dims=0)
+        rids = torch.arange(total - R, total, device=dev, dtype=torch.int64)
+    return (torch.cat([sk, mk, rk], dim=0), torch.cat([sv, mv, rv], dim=0), torch.cat([sids, mids, rids], dim=0))
+
+
+TriTierCache._reconstruct_engine = _reconstruct_engine
 
 
 def _counter_property(name):
