@@ -217,12 +217,109 @@ def trace_summary(db_path):
               f"{100.0 * sum(v) / total:.1f} |")
 
 
+ENGINE_CONFIGS = {
+    # Long-context decode through the engine: per layer one TriTierCacheEngine prefilled with `ctx` tokens,
+    # then `steps` decode steps of (ring ingest -> eviction routing -> waiting-room pack -> fused attention ->
+    # score feedback) over all layers. K outlier channels Student-t (nu = 3).
+    "qwen2-7b-128k-engine": dict(mode="step", Hq=28, Hkv=4, D=128, ctx=131072, layers=28, steps=256, S=4, R=256,
+                                 hr=0.05, decay=0.999, iv=32, kgs=16, meta="fp32", outliers="t3"),
+    # Tier maintenance alone: 2048 appends at 32 KV heads x 128 (ingest, routing, flush), each followed by the
+    # decayed score update with injected per-token weights, softmax of N(0, 2^2) logits over the visible set.
+    "maint-2048-32kv": dict(mode="inject", Hq=32, Hkv=32, D=128, ctx=0, layers=1, steps=2048, S=4, R=256, hr=0.05,
+                            decay=0.999, iv=32, kgs=16, meta="fp32", outliers=None, msl=2048),
+}
+
+
+def engine_bench(args, torch, L, lib):
+    """Engine configurations: µs per decode step over all layers (eager calls, one stream)."""
+    import numpy as np
+
+    cfg = ENGINE_CONFIGS[args.config]
+    Hq, Hkv, D, layers, steps = cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["layers"], cfg["steps"]
+    msl = cfg.get("msl", cfg["ctx"] + steps + 64)
+    sp = lambda: C.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    engines = []
+    t0 = time.time()
+    for layer in range(layers):
+        h = C.c_void_p()
+        L.check(lib.tt_engine_create(C.byref(h), Hq, Hkv, D, msl, cfg["S"], cfg["R"], cfg["hr"], cfg["decay"],
+                                     cfg["iv"], cfg["kgs"], cfg["meta"].encode(), sp()), "engine_create")
+        engines.append(h)
+        if cfg["ctx"]:
+            K = torch.randn((cfg["ctx"], Hkv, D), generator=g, device="cuda")
+            V = torch.randn((cfg["ctx"], Hkv, D), generator=g, device="cuda")
+            if cfg["outliers"] == "t3":
+                for hh in range(Hkv):
+                    ch = torch.randperm(D, generator=g, device="cuda")[:4]
+                    z = torch.randn((cfg["ctx"], 4), generator=g, device="cuda")
+                    chi = (torch.randn((cfg["ctx"], 4, 3), generator=g, device="cuda") ** 2).sum(-1)
+                    K[:, hh, ch] = z / torch.sqrt(chi / 3.0)
+            L.check(lib.tt_engine_prefill(h, K.data_ptr(), V.data_ptr(), cfg["ctx"], sp()), "prefill")
+            del K, V
+    torch.cuda.synchronize()
+    print(f"[bench] {layers} engines ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+    n_in = 8  # distinct input sets, cycled
+    Q = torch.randn((n_in, layers, Hq * D), generator=g, device="cuda")
+    Kn = torch.randn((n_in, layers, Hkv * D), generator=g, device="cuda")
+    Vn = torch.randn((n_in, layers, Hkv * D), generator=g, device="cuda")
+    out = torch.empty((layers, Hq * D), device="cuda")
+    if cfg["mode"] == "inject":
+        w = torch.softmax(2.0 * torch.randn((n_in, msl + 1024), generator=g, device="cuda"), dim=-1)
+
+    def run(s):
+        i = s % n_in
+        for layer, h in enumerate(engines):
+            if cfg["mode"] == "step":
+                L.check(lib.tt_engine_step(h, Q[i, layer].data_ptr(), Kn[i, layer].data_ptr(), Vn[i, layer].data_ptr(),
+                                           out[layer].data_ptr(), sp()), "step")
+            else:
+                L.check(lib.tt_engine_ingest(h, Kn[i, layer].data_ptr(), Vn[i, layer].data_ptr(), sp()), "ingest")
+                L.check(lib.tt_engine_feedback(h, w[i].data_ptr(), sp()), "feedback")
+
+    warm = min(args.warmup, 8)
+    for s in range(warm):
+        run(s)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for s in range(warm, steps):
+        run(s)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / (steps - warm)
+    cnt = np.zeros(23, np.int64)
+    L.check(lib.tt_engine_counters(engines[0], cnt.ctypes.data, sp()), "counters")
+    names = lib.tt_engine_counter_names().decode().split()
+    c = dict(zip(names, (int(x) for x in cnt)))
+    result = {
+        "metric": f"engine decode step µs/step ({args.config})",
+        "value": round(us, 2), "unit": "us/step", "n_gpus": 1, "steps": steps - warm, "warmup": warm,
+        "ms_per_step": round(us / 1000.0, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded on the GPU)",
+        "config": {"workload": args.config, **{k: v for k, v in cfg.items()}, "max_seq_len": msl},
+        "final_state_layer0": {k: c[k] for k in ("total_processed_tokens", "s_count", "hh_count", "rw_count",
+                                                 "wr_count", "pbs_count", "pbs_blocks_used", "total_evictions")},
+    }
+    if cfg["mode"] == "step":
+        nd = c["s_count"] + c["hh_count"] + c["rw_count"]
+        nb = c["pbs_blocks_used"]
+        mb = 2 if cfg["meta"] == "fp16" else 4
+        b = Hq * D * 4 + 2 * nd * Hkv * D * 4 + nb * Hkv * D * 4 * (cfg["kgs"] // 16) + nb * Hkv * D * 2 * mb \
+            + nb * cfg["kgs"] * Hkv * (D // 16) * 4 + nb * cfg["kgs"] * Hkv * 2 * mb + nb * cfg["kgs"] * 8
+        result["attention_bytes_per_step"] = b * layers
+        result["attention_GBps"] = round(b * layers / (us * 1e-6) / 1e9, 1)
+    for h in engines:
+        lib.tt_engine_destroy(h)
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="llama3-8b-32k", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="llama3-8b-32k", choices=sorted(CONFIGS) + sorted(ENGINE_CONFIGS))
     ap.add_argument("--meta", default="fp32", choices=["fp32", "fp16"], help="metadata dtype of the headline number")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -256,6 +353,9 @@ def main():
     lib = L.load()
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     torch.cuda.set_device(0)
+    if args.config in ENGINE_CONFIGS:
+        engine_bench(args, torch, L, lib)
+        return
     Hq, Hkv, D, ctx, layers, outl = CONFIGS[args.config]
     t0 = time.time()
     data, (nd, npk, nb) = build_layers(torch, L, Hq, Hkv, D, ctx, 1 if args.pmc_driver else layers, outl, args.seed)

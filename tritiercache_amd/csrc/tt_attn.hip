@@ -400,8 +400,12 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
 // dispatches the heads of one slot back to back: a token's V words, V scale /
 // zero and id sit in the same 128-byte lines for all KV heads, so they come
 // from memory once per token instead of once per head.
+//
+// Eight-head groups are held to three waves per SIMD (168 VGPRs; the few
+// spilled values live in the partial-tile logits store).
 template <int GP, typename MetaT>
-__global__ void __launch_bounds__(256) attn_packed_kernel(SplitArgs a, const int hc, const int chunks) {
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GP == 8 ? 3 : 1)))
+attn_packed_kernel(SplitArgs a, const int hc, const int chunks) {
     constexpr int kLds = MfLds<GP>::TOTAL > DnLds<GP>::TOTAL ? MfLds<GP>::TOTAL : DnLds<GP>::TOTAL;
     __shared__ __align__(16) char lds[kLds];
     const unsigned id = blockIdx.x;
@@ -564,33 +568,22 @@ __device__ __forceinline__ float sum8(float x) {
 constexpr int kMeanTokens = TT_MEAN_TOKENS;  // tokens per mean-weight workgroup
 constexpr int kMeanQuads = kMeanTokens / 4;  // token quads per workgroup
 constexpr int kMeanGroups = 256 / kMeanQuads;  // head groups per workgroup
+// Mean-weight workgroups at most; past that each takes an equal number of
+// token blocks, so fewer of them rebuild the per-head row statistics.
+#ifndef TT_MEAN_WGS
+#define TT_MEAN_WGS 1024
+#endif
+constexpr int kMeanMaxWgs = TT_MEAN_WGS;
 
-__device__ void fin_mean_tokens(const FinArgs& a, const int blk, float* sh) {
-    const int t = threadIdx.x;
+// Logits of token quad i0 for the heads hb + hg + kMeanGroups u, u < 8
+// (-inf past the end and for missing heads).
+__device__ __forceinline__ void fin_load_logits(const FinArgs& a, const int hb, const int hg, const int i0,
+                                                const int n, float4 (&lgv)[8]) {
     const int Hq = a.Hq;
-    int n = a.n_static;
-    int s = 0, hh = 0, rw = 0, total = 0, Nd = 0;
-    if (a.state) {
-        s = a.state[kSCount];
-        hh = a.state[kHhCount];
-        rw = a.state[kRwCount];
-        total = a.state[kTotal];
-        Nd = s + hh + rw;
-        n = Nd + a.state[kBlocksUsed] * a.kgs;
-    }
-    const int tok0 = blk * kMeanTokens;
-    if (tok0 >= n) return;
-    // Thread (head group hg, token quad q): heads hg, hg + kMeanGroups, ...;
-    // tokens tok0 + 4 q .. + 3. Rows are padded to a multiple of 4 floats.
-    // The logits of the first 8 kMeanGroups heads are loaded before anything
-    // else.
-    const int q = t % kMeanQuads, hg = t / kMeanQuads;
-    const int i0 = tok0 + 4 * q;
     const bool whole = i0 + 4 <= n;
-    float4 lgv[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-        const int h = hg + kMeanGroups * u;
+        const int h = hb + hg + kMeanGroups * u;
         lgv[u] = make_float4(kNegInf, kNegInf, kNegInf, kNegInf);
         if (h < Hq && i0 < n) {
             const float* lg = a.logits + static_cast<size_t>(h) * a.ld + i0;
@@ -603,6 +596,62 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int blk, float* sh) {
             }
         }
     }
+}
+
+// Token i's position in the score vector (-1 for none) and, for a heavy
+// hitter, its slot.
+struct FbToken {
+    long long tid;
+    int hh_slot;
+};
+
+// Mean-weight workgroup `wg` of `nwg`: token blocks wg, wg + nwg, ... of
+// kMeanTokens tokens each. The loads of a block's feedback ids and scores are
+// issued when the block starts, those of the next block's logits as soon as
+// the current ones are consumed.
+__device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, float* sh) {
+    const int t = threadIdx.x;
+    const int Hq = a.Hq;
+    int n = a.n_static;
+    int s = 0, hh = 0, rw = 0, total = 0, Nd = 0;
+    if (a.state) {
+        s = a.state[kSCount];
+        hh = a.state[kHhCount];
+        rw = a.state[kRwCount];
+        total = a.state[kTotal];
+        Nd = s + hh + rw;
+        n = Nd + a.state[kBlocksUsed] * a.kgs;
+    }
+    if (wg * kMeanTokens >= n) return;
+    // Feedback target of token i (threads t < kMeanTokens, one token each).
+    auto fb_token = [&](const int i) {
+        FbToken f{-1, -1};
+        if (i >= n) return f;
+        if (i < s) {
+            f.tid = i;
+        } else if (i < s + hh) {
+            f.hh_slot = i - s;
+            f.tid = a.fb.hh_ids[f.hh_slot];
+        } else if (i < Nd) {
+            f.tid = static_cast<long long>(total) - rw + (i - s - hh);
+        } else {
+            f.tid = a.fb.pbs_ids[i - Nd];
+        }
+        if (f.tid < 0 || f.tid >= a.fb.max_seq_len) f.tid = -1;
+        return f;
+    };
+    const bool fb_lane = a.fb.g && t < kMeanTokens;
+    FbToken ft{-1, -1};
+    float g_old = 0.0f;
+    if (fb_lane) {
+        ft = fb_token(wg * kMeanTokens + t);
+        if (ft.tid >= 0) g_old = a.fb.g[ft.tid];
+    }
+    // Thread (head group hg, token quad q): heads hg, hg + kMeanGroups, ...;
+    // tokens tok0 + 4 q .. + 3. Rows are padded to a multiple of 4 floats.
+    const int q = t % kMeanQuads, hg = t / kMeanQuads;
+    float4 lgv[8];
+    fin_load_logits(a, 0, hg, wg * kMeanTokens + 4 * q, n, lgv);
     // (M_h, 1/L_h) of every head: 8 threads per head, splits j0, j0 + 8, ...
     // (every workgroup rebuilds them: a second launch that waits for the
     // merge costs more than these loads)
@@ -638,70 +687,54 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int blk, float* sh) {
         }
     }
     __syncthreads();
-    float w4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (i0 < n) {
-        for (int hb = 0; hb < Hq; hb += 8 * kMeanGroups) {
+    float* red = sh + 2 * Hq;  // [kMeanGroups][kMeanTokens]
+    for (int blk = wg; blk * kMeanTokens < n; blk += nwg) {
+        const int tok0 = blk * kMeanTokens;
+        const int i0 = tok0 + 4 * q;
+        if (blk != wg && fb_lane) {
+            ft = fb_token(tok0 + t);
+            g_old = ft.tid >= 0 ? a.fb.g[ft.tid] : 0.0f;
+        }
+        float w4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        if (i0 < n) {
+            for (int hb = 0; hb < Hq; hb += 8 * kMeanGroups) {
+                if (hb > 0) fin_load_logits(a, hb, hg, i0, n, lgv);
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int h = hb + hg + kMeanGroups * u;
-                if (h >= Hq) break;
-                float4 v;
-                if (hb == 0) {
-                    v = lgv[u];
-                } else {
-                    const float* lg = a.logits + static_cast<size_t>(h) * a.ld + i0;
-                    v = make_float4(kNegInf, kNegInf, kNegInf, kNegInf);
-                    if (whole) {
-                        v = *reinterpret_cast<const float4*>(lg);
-                    } else {
-                        v.x = lg[0];
-                        if (i0 + 1 < n) v.y = lg[1];
-                        if (i0 + 2 < n) v.z = lg[2];
+                for (int u = 0; u < 8; ++u) {
+                    const int h = hb + hg + kMeanGroups * u;
+                    if (h >= Hq) break;
+                    const float sc[4] = {lgv[u].x, lgv[u].y, lgv[u].z, lgv[u].w};
+                    const float mh = Mh[h], il = iL[h];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        // s <= M_h, so 2^(s - M_h) <= 1 (flushed to 0 below 2^-126)
+                        const float w = (sc[e] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(sc[e] - mh) * il;
+                        w4[e] += w;
+                        if (a.head_w && i0 + e < n && i0 + e < a.head_w_ld)
+                            a.head_w[static_cast<size_t>(h) * a.head_w_ld + i0 + e] = w;
                     }
-                }
-                const float sc[4] = {v.x, v.y, v.z, v.w};
-                const float mh = Mh[h], il = iL[h];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    // s <= M_h, so 2^(s - M_h) <= 1 (flushed to 0 below 2^-126)
-                    const float w = (sc[e] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(sc[e] - mh) * il;
-                    w4[e] += w;
-                    if (a.head_w && i0 + e < n && i0 + e < a.head_w_ld)
-                        a.head_w[static_cast<size_t>(h) * a.head_w_ld + i0 + e] = w;
                 }
             }
         }
-    }
-    float* red = sh + 2 * Hq;  // [kMeanGroups][kMeanTokens]
+        const int nxt = blk + nwg;
+        if (nxt * kMeanTokens < n) fin_load_logits(a, 0, hg, nxt * kMeanTokens + 4 * q, n, lgv);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) red[hg * kMeanTokens + 4 * q + e] = w4[e];
-    __syncthreads();
-    if (t >= kMeanTokens) return;
-    const int i = tok0 + t;
-    if (i >= n) return;
-    float sum = 0.0f;
+        for (int e = 0; e < 4; ++e) red[hg * kMeanTokens + 4 * q + e] = w4[e];
+        __syncthreads();
+        const int i = tok0 + t;
+        if (t < kMeanTokens && i < n) {
+            float sum = 0.0f;
 #pragma unroll
-    for (int g = 0; g < kMeanGroups; ++g) sum += red[g * kMeanTokens + t];
-    const float mean = sum / static_cast<float>(Hq);
-    if (a.mw) a.mw[i] = mean;
-    if (a.fb.g) {
-        long long tid;
-        int hh_slot = -1;
-        if (i < s) {
-            tid = i;
-        } else if (i < s + hh) {
-            hh_slot = i - s;
-            tid = a.fb.hh_ids[hh_slot];
-        } else if (i < Nd) {
-            tid = static_cast<long long>(total) - rw + (i - s - hh);
-        } else {
-            tid = a.fb.pbs_ids[i - Nd];
+            for (int g = 0; g < kMeanGroups; ++g) sum += red[g * kMeanTokens + t];
+            const float mean = sum / static_cast<float>(Hq);
+            if (a.mw) a.mw[i] = mean;
+            if (fb_lane && ft.tid >= 0) {
+                const float gn = __builtin_fmaf(a.fb.decay, g_old, mean);
+                a.fb.g[ft.tid] = gn;
+                if (ft.hh_slot >= 0) a.fb.hh_scores[ft.hh_slot] = gn;
+            }
         }
-        if (tid >= 0 && tid < a.fb.max_seq_len) {
-            const float gn = __builtin_fmaf(a.fb.decay, a.fb.g[tid], mean);
-            a.fb.g[tid] = gn;
-            if (hh_slot >= 0) a.fb.hh_scores[hh_slot] = gn;
-        }
+        __syncthreads();  // `red` is rewritten by the next block
     }
 }
 
@@ -711,7 +744,7 @@ __global__ void __launch_bounds__(256) attn_finalize_kernel(FinArgs a) {
     if (b < a.Hq)
         fin_merge_head(a, b, sh);
     else
-        fin_mean_tokens(a, b - a.Hq, sh);
+        fin_mean_tokens(a, b - a.Hq, static_cast<int>(gridDim.x) - a.Hq, sh);
 }
 
 template <int CPL, int GP>
@@ -964,7 +997,12 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
     f.head_w = head_w;
     f.head_w_ld = head_w_ld;
     f.fb = fb ? *fb : Feedback{};
-    const int mean_wgs = weights ? (std::max(plan.token_ub, 1) + kMeanTokens - 1) / kMeanTokens : 0;
+    int mean_wgs = 0;
+    if (weights) {
+        const int blocks = (std::max(plan.token_ub, 1) + kMeanTokens - 1) / kMeanTokens;
+        const int per_wg = (blocks + kMeanMaxWgs - 1) / kMeanMaxWgs;
+        mean_wgs = (blocks + per_wg - 1) / per_wg;
+    }
     const size_t lds = sizeof(float) * std::max<size_t>(8 + 4 * 256, 2 * static_cast<size_t>(in.Hq) + 256 * 4);
     hipLaunchKernelGGL(attn_finalize_kernel, dim3(in.Hq + mean_wgs), dim3(256), lds, stream, f);
     TT_LAUNCH_CHECK();

@@ -63,9 +63,13 @@ struct MfLds {
     static constexpr int VS = 4736;    // [32] f32, MFMA token order (0 for masked slots)
     static constexpr int VZ = 4864;    // [32] f32
     static constexpr int BIAS = 4992;  // [2 tiles][8] f32 per-head QK bias
-    static constexpr int BHL = 5056;   // [2 tiles][hi rows 0..GP-1, lo rows GP..2GP-1][kBRS] f16
+    static constexpr int BHL = 5056;   // [NBT tiles][hi rows 0..GP-1, lo rows GP..2GP-1][kBRS] f16
     static constexpr int BHL_TILE = 2 * GP * kBRS * 2;
-    static constexpr int BYTES = BHL + 2 * BHL_TILE;
+    // Coefficient tiles held at once. Eight heads keep one (the second tile
+    // of a pair reuses it), which brings the workgroup under a third of the
+    // CU's 160 KB and lets three workgroups share a CU.
+    static constexpr int NBT = GP > 4 ? 1 : 2;
+    static constexpr int BYTES = BHL + NBT * BHL_TILE;
     // final merge of the four waves, reusing the staging area
     static constexpr int MERGE = 4 * GP * (3 + kMfD) * 4;
     static_assert(MERGE <= 4 * BYTES, "merge area must fit in the staging area");
@@ -293,9 +297,9 @@ __device__ __forceinline__ void dense_share(const SplitArgs& a, const DenseView&
     const int G = in.Hq / in.Hkv;
     const int Nd = dv.Nd;
     float* my = dl + wave * GP * (2 + kMfD);
-#pragma unroll 1
-    for (int pass = 0; pass < NPASS; ++pass) {
-        const int gb = pass * HP;
+    // Heads [gb, gb + HP); the first pass starts with the prefetched tile.
+    // (Peeling that pass keeps `t0` out of the later passes' live range.)
+    auto run_pass = [&](const int gb, const bool first) {
         float m[HP], l[HP], acc[HP][8];
 #pragma unroll
         for (int g = 0; g < HP; ++g) {
@@ -363,18 +367,13 @@ __device__ __forceinline__ void dense_share(const SplitArgs& a, const DenseView&
                 m[g] = mn;
             }
         };
-        const int kf = d0 + wave;
-        if (kf < d1) {
-            if (pass == 0) {
-                consume(t0, kf);  // in flight since the start of the kernel
-            } else {
-                DenseTile t;
-                dense_load(in, dv, kvh, kf, t);
-                consume(t, kf);
-            }
+        int kb = d0 + wave;
+        if (first && kb < d1) {
+            consume(t0, kb);  // in flight since the start of the kernel
+            kb += 4;
         }
 #pragma unroll 1
-        for (int k = kf + 4; k < d1; k += 4) {
+        for (int k = kb; k < d1; k += 4) {
             DenseTile t;
             dense_load(in, dv, kvh, k, t);
             consume(t, k);
@@ -395,7 +394,10 @@ __device__ __forceinline__ void dense_share(const SplitArgs& a, const DenseView&
                 }
             }
         }
-    }
+    };
+    run_pass(0, true);
+#pragma unroll 1
+    for (int pass = 1; pass < NPASS; ++pass) run_pass(pass * HP, false);
 }
 
 // One FP32-tier workgroup: KV head kvh, query heads [GP * chunk, +GP), FP32
@@ -659,8 +661,8 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     };
 
     // QK coefficients of one tile's block: hi in rows h, lo in rows GP + h.
-    auto coeffs = [&](const int tile) {
-        char* bt = bhl_l + tile * L::BHL_TILE;
+    auto coeffs = [&](const int tile, const int slot) {
+        char* bt = bhl_l + slot * L::BHL_TILE;
 #pragma unroll
         for (int pp = 0; pp < NP; ++pp) {
             const int h = 4 * pp + gk;
@@ -684,7 +686,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
             if (GP >= 4 || h < GP) {
                 *reinterpret_cast<mf_u4*>(bt + (h * kBRS + 8 * n) * 2) = hi;
                 *reinterpret_cast<mf_u4*>(bt + ((GP + h) * kBRS + 8 * n) * 2) = lo;
-                bias_l[tile * 8 + h] = bp;  // the 16 lanes of the row hold the same total
+                bias_l[slot * 8 + h] = bp;  // the 16 lanes of the row hold the same total
             }
         }
     };
@@ -693,14 +695,19 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         const uint32_t vmask = stage();
         if (p + 1 < wp1) fetch(p + 1);
         wave_lds_sync();
-        coeffs(0);
-        if (W == 1) coeffs(1);
+        coeffs(0, 0);
+        if (W == 1 && L::NBT == 2) coeffs(1, 1);
         wave_lds_sync();
 
         float s2[2][4];
 #pragma unroll
         for (int tile = 0; tile < 2; ++tile) {
-            const int tb = (W == 2) ? 0 : tile;
+            const int tb = (W == 2 || L::NBT == 1) ? 0 : tile;
+            if (W == 1 && L::NBT == 1 && tile == 1) {
+                wave_lds_sync();  // tile 0's coefficients and bias are read
+                coeffs(1, 0);
+                wave_lds_sync();
+            }
             // A: codes of token t = lane & 15 (k = t & 3), channels 32 gk .. 32 gk + 31.
             const mf_u4* ka = reinterpret_cast<const mf_u4*>(kt_l + (tile * 4 + ((lane & 15) >> 2)) * kKTS + 8 * gk);
             const mf_u4 ra = ka[0], rb = ka[1];

@@ -49,44 +49,75 @@ __global__ void __launch_bounds__(256) append_row_kernel(const float* __restrict
     }
 }
 
-// Exact k-th smallest of g[0..n) by a 4-pass MSB radix select on order-
-// preserving keys; any exact selection equals std::nth_element's pick
-// (cache_engine.cpp:126-144). Writes the threshold and last_calc_pos.
+// Exact k-th smallest of g[0..n) by an MSB radix select on order-preserving
+// keys, three passes of 11, 11 and 10 bits; any exact selection equals
+// std::nth_element's pick (cache_engine.cpp:126-144). Writes the threshold
+// and last_calc_pos. One workgroup: every thread keeps kThrBatch loads in
+// flight per pass step, and the digit of each pass is found with a parallel
+// prefix sum over the histogram.
+constexpr int kThrBatch = 32;
+
+__device__ __forceinline__ unsigned int wave_incl_scan(unsigned int x) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const unsigned int y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+    }
+    return x;
+}
+
 __global__ void __launch_bounds__(1024) threshold_kernel(const float* __restrict__ g, int n, long long k, int* st,
                                                          int total) {
-    __shared__ unsigned int hist[256];
-    __shared__ unsigned int s_prefix, s_mask;
-    __shared__ long long s_k;
-    if (threadIdx.x == 0) {
+    __shared__ unsigned int hist[2048];
+    __shared__ unsigned int wtot[16];
+    __shared__ unsigned int s_prefix, s_mask, s_k;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) {
         s_prefix = 0;
         s_mask = 0;
-        s_k = k;
+        s_k = static_cast<unsigned int>(k);  // k < n < 2^31
     }
-    for (int pass = 0; pass < 4; ++pass) {
-        const int shift = 24 - 8 * pass;
-        for (int i = threadIdx.x; i < 256; i += blockDim.x) hist[i] = 0;
+    for (int pass = 0; pass < 3; ++pass) {
+        const int bits = pass < 2 ? 11 : 10;
+        const int shift = pass == 0 ? 21 : (pass == 1 ? 10 : 0);
+        const unsigned int dm = (1u << bits) - 1u;
+        for (int i = tid; i < 2048; i += 1024) hist[i] = 0;
         __syncthreads();
         const unsigned int prefix = s_prefix, mask = s_mask;
-        for (int i = threadIdx.x; i < n; i += blockDim.x) {
-            const unsigned int u = __float_as_uint(g[i]);
-            const unsigned int key = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-            if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        for (int base = 0; base < n; base += 1024 * kThrBatch) {
+            unsigned int u[kThrBatch];
+#pragma unroll
+            for (int j = 0; j < kThrBatch; ++j) {
+                const int i = base + j * 1024 + tid;
+                u[j] = i < n ? __float_as_uint(g[i]) : 0u;
+            }
+#pragma unroll
+            for (int j = 0; j < kThrBatch; ++j) {
+                const unsigned int key = (u[j] & 0x80000000u) ? ~u[j] : (u[j] | 0x80000000u);
+                if (base + j * 1024 + tid < n && (key & mask) == prefix) atomicAdd(&hist[(key >> shift) & dm], 1u);
+            }
         }
         __syncthreads();
-        if (threadIdx.x == 0) {
-            long long kk = s_k, cum = 0;
-            int d = 0;
-            for (; d < 255; ++d) {
-                if (cum + hist[d] > static_cast<unsigned long long>(kk)) break;
-                cum += hist[d];
-            }
-            s_k = kk - cum;
-            s_prefix = prefix | (static_cast<unsigned int>(d) << shift);
-            s_mask = mask | (255u << shift);
+        // Thread t owns bins 2t and 2t + 1; the digit is the bin where the
+        // running count passes s_k (exactly one thread finds it).
+        const unsigned int h0 = hist[2 * tid], h1 = hist[2 * tid + 1];
+        const unsigned int incl = wave_incl_scan(h0 + h1);
+        if (lane == 63) wtot[wave] = incl;
+        __syncthreads();
+        unsigned int before = incl - (h0 + h1);
+        for (int w = 0; w < wave; ++w) before += wtot[w];
+        const unsigned int kk = s_k;
+        __syncthreads();  // everyone has read s_k
+        if (before <= kk && kk < before + h0 + h1) {
+            const unsigned int d = (kk < before + h0) ? 2u * tid : 2u * tid + 1u;
+            s_k = kk - before - (d & 1u ? h0 : 0u);
+            s_prefix = prefix | (d << shift);
+            s_mask = mask | (dm << shift);
         }
         __syncthreads();
     }
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
         const unsigned int key = s_prefix;
         const unsigned int u = (key & 0x80000000u) ? (key & 0x7fffffffu) : ~key;
         st[kThreshold] = static_cast<int>(u);
@@ -422,6 +453,10 @@ struct tt_engine {
     int* st = nullptr;
     // host mirror of the data-independent counters
     int h_s = 0, h_rw = 0, h_head = 0, h_total = 0, h_ev = 0, h_last = -1;
+    // Heavy hitters grow by at most one per routed eviction (prefill routes
+    // none), so this count, capped at max_hh, bounds the tier without a
+    // device read.
+    int h_routed = 0;
     int blocks_ub = 0, wr_ub = 0;
     // attention workspace
     void* ws = nullptr;
@@ -445,6 +480,8 @@ int engine_free_pbs(tt_engine* e) {
     (void)hipFree(e->PBS_ids);
     return TT_OK;
 }
+
+int engine_reserve_ws(tt_engine* e, const AttnPlan& p, hipStream_t s);
 
 // Physical packed-store capacity. Buffers are reallocated (and copied) only
 // when the upper bound on used blocks exceeds the allocation.
@@ -490,7 +527,12 @@ int engine_reserve_blocks(tt_engine* e, int need, hipStream_t s) {
     e->PBS_ids = ids;
     e->cap_blocks = nc;
     // Attention workspace follows the capacity.
-    const AttnPlan p = attn_plan(e->S + e->max_hh + e->R, nc, e->Hq, e->Hkv, e->D, e->kgs, true, e->fp16);
+    return engine_reserve_ws(e, attn_plan(e->S + e->max_hh + e->R, nc, e->Hq, e->Hkv, e->D, e->kgs, true, e->fp16), s);
+}
+
+// Grows the attention workspace and the mean-weight buffer to what plan `p`
+// needs (plans for smaller bounds are not always smaller).
+int engine_reserve_ws(tt_engine* e, const AttnPlan& p, hipStream_t s) {
     if (p.bytes > e->ws_bytes) {
         if (e->ws) {
             TT_HIP_CHECK(hipStreamSynchronize(s));
@@ -734,6 +776,7 @@ int tt_engine_ingest(tt_engine* e, const float* K_new, const float* V_new, void*
         TT_LAUNCH_CHECK();
         e->h_head = a.new_head;
         e->h_ev++;
+        if (e->h_routed < e->max_hh) e->h_routed++;
         if (++e->wr_ub >= e->chunk) {
             e->wr_ub -= e->chunk;
             e->blocks_ub++;
@@ -749,7 +792,10 @@ static int engine_attend(tt_engine* e, const float* Q, float* out, float* head_w
                          hipStream_t s) {
     int rc = engine_reserve_blocks(e, e->blocks_ub, s);
     if (rc) return rc;
-    const AttnPlan p = attn_plan(e->S + e->max_hh + e->R, e->blocks_ub, e->Hq, e->Hkv, e->D, e->kgs, true, e->fp16);
+    const int dense_ub = e->h_s + e->h_routed + e->h_rw;
+    const AttnPlan p = attn_plan(dense_ub, e->blocks_ub, e->Hq, e->Hkv, e->D, e->kgs, true, e->fp16);
+    rc = engine_reserve_ws(e, p, s);
+    if (rc) return rc;
     AttnInputs in = engine_inputs(e, Q);
     Feedback fb = engine_feedback_args(e);
     return attn_launch(in, p, e->ws, out, e->mw, feedback ? &fb : nullptr, head_w, head_w_ld, s);
