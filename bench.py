@@ -73,7 +73,7 @@ def bytes_read_per_layer(Hq, Hkv, D, ctx, meta_bytes, with_ids=True):
     return b
 
 
-def build_layers(torch, L, Hq, Hkv, D, ctx, layers, outliers, seed):
+def build_layers(torch, L, Hq, Hkv, D, ctx, layers, outliers, seed, metas=("32", "16")):
     nd, npk, nb = tier_sizes(ctx)
     g = torch.Generator(device="cuda").manual_seed(seed)
     dev = "cuda"
@@ -101,6 +101,8 @@ def build_layers(torch, L, Hq, Hkv, D, ctx, layers, outliers, seed):
         d["KP"] = torch.empty((nb, Hkv, D), dtype=torch.int32, device=dev)
         d["VP"] = torch.empty((nb * 16, Hkv, D // 16), dtype=torch.int32, device=dev)
         for tag, fp16, mdt in (("32", 0, torch.float32), ("16", 1, torch.uint16)):
+            if tag not in metas:
+                continue
             ks = torch.empty((nb, Hkv, D), dtype=mdt, device=dev)
             kz = torch.empty_like(ks)
             vs = torch.empty((nb * 16, Hkv), dtype=mdt, device=dev)
@@ -314,12 +316,142 @@ def engine_bench(args, torch, L, lib):
     print(json.dumps(result), flush=True)
 
 
+BATCH_CONFIGS = {
+    # Batched ragged decode: `batch` sequences with contexts ~ U[lo, hi] drawn from the seed, each with its own tier
+    # tables (4 sinks, 256 recent, 5% heavy hitters FP32, the rest 2-bit) in every layer; one
+    # tt_fused_attention_decode_batched call per layer, the 32 layers replayed as one HIP graph.
+    "mistral-7b-batch16": dict(Hq=32, Hkv=8, D=128, batch=16, lo=2048, hi=32768, layers=32),
+}
+
+
+def batch_bench(args, torch, L, lib):
+    """Batched ragged decode: µs per step (all sequences, all layers), HBM GB/s on the bytes the step reads."""
+    import numpy as np
+
+    cfg = BATCH_CONFIGS[args.config]
+    Hq, Hkv, D, B, layers = cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["batch"], cfg["layers"]
+    fp16 = 1 if args.meta == "fp16" else 0
+    tag = "16" if fp16 else "32"
+    mb = 2 if fp16 else 4
+    ctxs = [int(c) for c in np.random.default_rng(args.seed).integers(cfg["lo"], cfg["hi"] + 1, size=B)]
+    sp = lambda: C.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
+    t0 = time.time()
+    data = []  # [layer][seq] -> tier tables
+    for layer in range(layers):
+        row = []
+        for i, ctx in enumerate(ctxs):
+            d, sizes = build_layers(torch, L, Hq, Hkv, D, ctx, 1, None, args.seed + 7919 * layer + i, metas=(tag,))
+            d[0]["sizes"] = sizes
+            row.append(d[0])
+        data.append(row)
+    print(f"[bench] built {layers} layers x {B} sequences (ctx {min(ctxs)}..{max(ctxs)}) in {time.time() - t0:.1f}s",
+          file=sys.stderr, flush=True)
+    descs, ws_bytes = [], 0
+    for row in data:
+        arr = (L.DecodeSeq * B)()
+        for i, d in enumerate(row):
+            nd, _, nb = d["sizes"]
+            s = arr[i]
+            s.Q, s.dense_K, s.dense_V = d["Q"].data_ptr(), d["dK"].data_ptr(), d["dV"].data_ptr()
+            s.PBS_K_Packed, s.PBS_K_Scales, s.PBS_K_Zeroes = (d["KP"].data_ptr(), d["KS" + tag].data_ptr(),
+                                                              d["KZ" + tag].data_ptr())
+            s.PBS_V_Packed, s.PBS_V_Scales, s.PBS_V_Zeroes = (d["VP"].data_ptr(), d["VS" + tag].data_ptr(),
+                                                              d["VZ" + tag].data_ptr())
+            s.PBS_token_ids, s.attn_output, s.mean_attn_weights = (d["ids"].data_ptr(), d["out"].data_ptr(),
+                                                                   d["mw"].data_ptr())
+            s.dense_count, s.num_blocks = nd, nb
+        dev = torch.from_numpy(np.frombuffer(bytes(arr), dtype=np.uint8).copy()).cuda()
+        descs.append((arr, dev))
+        ws_bytes = max(ws_bytes, int(lib.tt_batched_decode_workspace_bytes(arr, B, Hq, Hkv, D, 16)))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+
+    def step():
+        for arr, dev in descs:
+            L.check(lib.tt_fused_attention_decode_batched(arr, dev.data_ptr(), B, Hq, Hkv, D, 16, fp16, ws.data_ptr(),
+                                                          ws_bytes, sp()), "batched")
+
+    step()
+    torch.cuda.synchronize()
+    run, graphed = step, False
+    if not args.no_graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        run, graphed = g.replay, True
+    for _ in range(args.warmup):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1000.0 / args.steps
+    per_seq = [bytes_read_per_layer(Hq, Hkv, D, c, mb) for c in ctxs]
+    bstep = sum(per_seq) * layers
+    gbps = bstep / (us * 1e-6) / 1e9
+
+    cpu = parity = None
+    if not args.no_cpu:
+        from oracle.binding import load_oracle, load_reference
+
+        impl = load_reference() or load_oracle()
+        tot = 0.0
+        toks = 0
+        n = 0
+        for i in range(B):  # layer 0, sequences in order, within the time bound
+            d = data[0][i]
+            nd, _, nb = d["sizes"]
+            h = {k: (v.cpu().numpy() if v.dtype != torch.uint16 else v.cpu().view(torch.int16).numpy().view(np.uint16))
+                 for k, v in d.items() if k != "sizes"}
+            cargs = (h["Q"], h["dK"], h["dV"], nd, h["KP"].reshape(nb, 1, Hkv, D), h["KS" + tag], h["KZ" + tag],
+                     h["VP"], h["VS" + tag], h["VZ" + tag], h["ids"], nb, Hq, Hkv, D, 16, bool(fp16))
+            t1 = time.perf_counter()
+            ro, rmw = impl.fused_attention_decode(*cargs)
+            tot += time.perf_counter() - t1
+            toks += nd + nb * 16
+            n += 1
+            if i == 0:
+                parity = {
+                    "seq0_layer0_out_max_rel_err": float(np.abs(h["out"] - ro).max() / np.abs(ro).max()),
+                    "seq0_layer0_mean_weights_max_rel_err": float(np.abs(h["mw"] - rmw).max() / np.abs(rmw).max()),
+                    "checked_against": impl.kind,
+                }
+            if tot >= args.cpu_seconds:
+                break
+        all_toks = sum(tier_sizes(c)[0] + tier_sizes(c)[2] * 16 for c in ctxs) * layers
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)) if impl.kind == "reference" else 1
+        cpu = {"value": tot / toks * all_toks * 1e6, "unit": "us/step", "cores": threads, "kind": impl.kind,
+               "sample": f"layer 0 of the first {n} sequences ({toks} tokens), {tot:.1f}s, scaled by tokens to "
+                         f"{B} sequences x {layers} layers"}
+    result = {
+        "metric": f"batched ragged decode-attn µs/step ({args.config})",
+        "value": round(us, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(us / 1000.0, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f32", "data": "synthetic (seeded N(0,1) on the GPU; packed by the library quantisers)",
+        "config": {"workload": f"{args.config}: {B} sequences, ctx {ctxs}, {Hq} q heads / {Hkv} KV heads, head_dim "
+                               f"{D}, {layers} layers, {args.meta} metadata, mean attention weights computed",
+                   "ctxs": ctxs, "layers": layers, "hip_graph": graphed},
+        "achieved_GBps": round(gbps, 1),
+        "pct_of_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
+        "bytes_read_per_step": bstep,
+        "roofline": {"bound": "hbm", "kernel": "step (attn_batched_kernel + attn_finalize_batched_kernel)",
+                     "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None},
+        "cpu_baseline": cpu,
+        "parity": parity,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--config", default="llama3-8b-32k", choices=sorted(CONFIGS) + sorted(ENGINE_CONFIGS))
+    ap.add_argument("--config", default="llama3-8b-32k",
+                    choices=sorted(CONFIGS) + sorted(ENGINE_CONFIGS) + sorted(BATCH_CONFIGS))
     ap.add_argument("--meta", default="fp32", choices=["fp32", "fp16"], help="metadata dtype of the headline number")
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
@@ -355,6 +487,9 @@ def main():
     torch.cuda.set_device(0)
     if args.config in ENGINE_CONFIGS:
         engine_bench(args, torch, L, lib)
+        return
+    if args.config in BATCH_CONFIGS:
+        batch_bench(args, torch, L, lib)
         return
     Hq, Hkv, D, ctx, layers, outl = CONFIGS[args.config]
     t0 = time.time()

@@ -144,6 +144,51 @@ TT_API int tt_attention_finalize(const float* Q, int dense_count, int num_blocks
                                  void* stream);
 
 /* ---------------------------------------------------------------------------
+ * Batched ragged decode: one decode step of many sequences, each with its own
+ * tier tables and lengths, in one split-K launch plus one merge launch (head_dim
+ * 128; other head dims run the sequences one after another). No counterpart
+ * in the reference, whose callers run fused_attention_decode (bindings.cpp:
+ * 99-178) once per sequence; each sequence's result is that call's result.
+ *
+ * One tt_decode_seq holds the arguments of tt_fused_attention_decode for one
+ * sequence (all device pointers; mean_attn_weights may be NULL, the PBS
+ * pointers are unused when num_blocks == 0 and the dense ones when
+ * dense_count == 0). */
+typedef struct tt_decode_seq {
+    const float* Q;                  /* [Hq, D] */
+    const float* dense_K;            /* [dense_count, Hkv, D] */
+    const float* dense_V;            /* [dense_count, Hkv, D] */
+    const int32_t* PBS_K_Packed;     /* [num_blocks * k_group_size / 16, Hkv, D] */
+    const void* PBS_K_Scales;        /* [num_blocks, Hkv, D] */
+    const void* PBS_K_Zeroes;        /* [num_blocks, Hkv, D] */
+    const int32_t* PBS_V_Packed;     /* [num_blocks * k_group_size, Hkv, D / 16] */
+    const void* PBS_V_Scales;        /* [num_blocks * k_group_size, Hkv] */
+    const void* PBS_V_Zeroes;        /* [num_blocks * k_group_size, Hkv] */
+    const int64_t* PBS_token_ids;    /* [num_blocks * k_group_size], -1 = masked slot */
+    float* attn_output;              /* [Hq, D] */
+    float* mean_attn_weights;        /* [dense_count + num_blocks * k_group_size] or NULL */
+    int32_t dense_count;
+    int32_t num_blocks;
+} tt_decode_seq;
+
+/* Device workspace bytes for tt_fused_attention_decode_batched over `seqs`
+ * (host array; only the counts and the mean_attn_weights pointers are read).
+ * 0 on invalid arguments. */
+TT_API size_t tt_batched_decode_workspace_bytes(const tt_decode_seq* seqs, int num_seqs, int num_q_heads,
+                                                int num_kv_heads, int head_dim, int k_group_size);
+
+/* `seqs` (host memory) is read by the call to plan the launch; the kernels
+ * read `seqs_device`, a device copy of the same array, which must stay valid
+ * and unchanged until the work enqueued on `stream` has run. All sequences
+ * share the head counts, head_dim, k_group_size and metadata dtype. The
+ * workspace must hold tt_batched_decode_workspace_bytes(...) bytes. No
+ * allocation. */
+TT_API int tt_fused_attention_decode_batched(const tt_decode_seq* seqs, const tt_decode_seq* seqs_device,
+                                             int num_seqs, int num_q_heads, int num_kv_heads, int head_dim,
+                                             int k_group_size, int meta_fp16, void* workspace,
+                                             size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
  * Engine: replaces _C.TriTierCacheEngine (bindings.cpp:384-626, class
  * csrc/include/cache_engine.h:10-123, csrc/cache_engine.cpp). All tier buffers
  * and counters live in device memory; a step enqueues its kernels without a

@@ -64,3 +64,43 @@ def test_errors_without_gpu_are_python_exceptions():
         _C.TriTierCacheEngine(4, 4, 64, 128)
     with pytest.raises(ValueError):
         _C.fused_attention_decode(0, None, None, -1, None, None, None, None, None, None, None, 0, 4, 4, 64, 0)
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="native library not built")
+def test_decode_seq_layout_matches_header(tmp_path):
+    """The ctypes mirror of tt_decode_seq has the C struct's size and field offsets (gcc on the header)."""
+    import ctypes as C
+    import shutil
+
+    from tritiercache_amd import _lib
+
+    if shutil.which("gcc") is None:
+        pytest.skip("gcc not available")
+    names = [f[0] for f in _lib.DecodeSeq._fields_]
+    src = tmp_path / "layout.c"
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "tritiercache_amd.h"\nint main(void) {\n'
+                   '  printf("%zu\\n", sizeof(tt_decode_seq));\n'
+                   + "".join(f'  printf("%zu\\n", offsetof(tt_decode_seq, {n}));\n' for n in names) + "  return 0;\n}\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
+    got = [int(x) for x in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    want = [C.sizeof(_lib.DecodeSeq)] + [getattr(_lib.DecodeSeq, n).offset for n in names]
+    assert got == want
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="native library not built")
+def test_batched_workspace_rejects_bad_shapes():
+    """Host-side validation of the batched entry point (no kernel runs)."""
+    from tritiercache_amd import _lib
+
+    L = _lib.load()
+    seqs = (_lib.DecodeSeq * 2)()
+    for s in seqs:
+        s.Q, s.attn_output, s.dense_count, s.num_blocks = 0x1000, 0x2000, 0, 0
+    assert L.tt_batched_decode_workspace_bytes(seqs, 2, 7, 2, 128, 16) == 0   # GQA ratio not integral
+    assert _lib.last_error()
+    assert L.tt_batched_decode_workspace_bytes(seqs, -1, 8, 2, 128, 16) == 0
+    seqs[1].num_blocks = 3  # PBS pointers missing
+    assert L.tt_batched_decode_workspace_bytes(seqs, 2, 8, 2, 128, 16) == 0
+    seqs[1].num_blocks = 0
+    assert L.tt_batched_decode_workspace_bytes(seqs, 2, 8, 2, 128, 16) > 0

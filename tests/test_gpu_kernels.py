@@ -10,7 +10,7 @@ import pytest
 import torch
 
 from oracle import synth
-from gpu_helpers import dev, host, quantize_blocks_gpu, rel_err, same_bits
+from gpu_helpers import dev, host, make_case, quantize_blocks_gpu, rel_err, same_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -171,35 +171,6 @@ def test_fused_attention_golden(C, golden):
         out, mw = _run_fused_gpu(C, args)
         assert rel_err(out, K[f"fa{i}_out"]) <= ATTN_TOL, i
         assert rel_err(mw, K[f"fa{i}_mw"]) <= ATTN_TOL, i
-
-
-def make_case(oracle, Hq, Hkv, D, nd, nb, kgs, fp16, mask, seed, k_outliers=False):
-    Q = synth.normal(seed, 0, (Hq, D))
-    dK, dV = synth.normal(seed, 1, (nd, Hkv, D)), synth.normal(seed, 2, (nd, Hkv, D))
-    nbk = max(nb, 1)
-    Kp, Vp = synth.normal(seed, 3, (nbk * kgs, Hkv, D)), synth.normal(seed, 4, (nbk * kgs, Hkv, D))
-    if k_outliers:
-        Kp[:, :, :4] *= 8.0
-        dK[:, :, :4] *= 8.0
-    packs = [(oracle.quantize_k(Kp[b * kgs:(b + 1) * kgs], kgs, fp16), oracle.quantize_v(Vp[b * kgs:(b + 1) * kgs], fp16))
-             for b in range(nbk)]
-    KP = np.stack([k[0] for k, _ in packs])
-    KS = np.stack([k[1] for k, _ in packs])
-    KZ = np.stack([k[2] for k, _ in packs])
-    VP = np.concatenate([v[0] for _, v in packs])
-    VS = np.concatenate([v[1] for _, v in packs])
-    VZ = np.concatenate([v[2] for _, v in packs])
-    ids = np.arange(nbk * kgs, dtype=np.int64) + nd
-    rng = np.random.default_rng(seed)
-    if mask == "tail":
-        ids[-(kgs // 2 + 3):] = -1
-    elif mask == "holes":
-        ids[rng.random(ids.size) < 0.2] = -1
-    elif mask == "block":
-        ids[:kgs] = -1
-    elif mask == "all":
-        ids[:] = -1
-    return (Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, fp16)
 
 
 SWEEP = [

@@ -208,6 +208,70 @@ def fused_attention_decode(Q_ptr, dense_K_ptr, dense_V_ptr, dense_count, PBS_K_P
     st.finish()
 
 
+_BATCH_FIELDS = ("Q", "dense_K", "dense_V", "dense_count", "PBS_K_Packed", "PBS_K_Scales", "PBS_K_Zeroes",
+                 "PBS_V_Packed", "PBS_V_Scales", "PBS_V_Zeroes", "PBS_token_ids", "num_blocks", "attn_output",
+                 "mean_attn_weights")
+
+
+def fused_attention_decode_batched(batch, num_q_heads, num_kv_heads, head_dim, k_group_size=16,
+                                   pbs_metadata_dtype="fp32"):
+    """One decode step of many sequences in one split-K launch (plus one merge launch).
+
+    `batch` holds one entry per sequence: a dict with the keys of
+    ``_BATCH_FIELDS`` or a tuple in that order, i.e. the per-sequence
+    arguments of fused_attention_decode (bindings.cpp:99-178); each
+    sequence's outputs equal that call's. The sequences share the head
+    counts, head_dim, k_group_size and metadata dtype. No counterpart in the
+    reference, whose callers loop over sequences."""
+    Hq, Hkv, D, kgs = int(num_q_heads), int(num_kv_heads), int(head_dim), int(k_group_size)
+    if Hq <= 0 or Hkv <= 0 or D <= 0:
+        raise ValueError("num_q_heads, num_kv_heads, and head_dim must be positive integers.")
+    _require_gpu()
+    entries = [dict(e) if isinstance(e, dict) else dict(zip(_BATCH_FIELDS, e)) for e in batch]
+    if not entries:
+        return
+    fp16 = _is_fp16(pbs_metadata_dtype, entries[0].get("PBS_K_Scales"))
+    msz = 2 if fp16 else 4
+    kvs = Hkv * D
+    W = max(kgs // 16, 1)
+    st = _Staging()
+    seqs = (_lib.DecodeSeq * len(entries))()
+    for i, e in enumerate(entries):
+        nd, nb = int(e.get("dense_count", 0)), int(e.get("num_blocks", 0))
+        if nd < 0:
+            raise ValueError("dense_count must be non-negative.")
+        if nb < 0:
+            raise ValueError("num_blocks must be non-negative.")
+        nd0, nb0 = nd == 0, nb == 0
+        s = seqs[i]
+        s.Q = st.ptr(e.get("Q"), "Q", Hq * D * 4)
+        s.dense_K = st.ptr(e.get("dense_K"), "dense_K", nd * kvs * 4, nullable=nd0) or None
+        s.dense_V = st.ptr(e.get("dense_V"), "dense_V", nd * kvs * 4, nullable=nd0) or None
+        s.PBS_K_Packed = st.ptr(e.get("PBS_K_Packed"), "PBS_K_Packed", nb * W * kvs * 4, nullable=nb0) or None
+        s.PBS_K_Scales = st.ptr(e.get("PBS_K_Scales"), "PBS_K_Scales", nb * kvs * msz, nullable=nb0) or None
+        s.PBS_K_Zeroes = st.ptr(e.get("PBS_K_Zeroes"), "PBS_K_Zeroes", nb * kvs * msz, nullable=nb0) or None
+        s.PBS_V_Packed = st.ptr(e.get("PBS_V_Packed"), "PBS_V_Packed", nb * kgs * Hkv * (D // 16) * 4,
+                                nullable=nb0) or None
+        s.PBS_V_Scales = st.ptr(e.get("PBS_V_Scales"), "PBS_V_Scales", nb * kgs * Hkv * msz, nullable=nb0) or None
+        s.PBS_V_Zeroes = st.ptr(e.get("PBS_V_Zeroes"), "PBS_V_Zeroes", nb * kgs * Hkv * msz, nullable=nb0) or None
+        s.PBS_token_ids = st.ptr(e.get("PBS_token_ids"), "PBS_token_ids", nb * kgs * 8, nullable=nb0) or None
+        s.attn_output = st.ptr(e.get("attn_output"), "attn_output", Hq * D * 4, writable=True)
+        s.mean_attn_weights = st.ptr(e.get("mean_attn_weights"), "mean_attn_weights", (nd + nb * kgs) * 4,
+                                     writable=True, nullable=True) or None
+        s.dense_count, s.num_blocks = nd, nb
+    n = len(entries)
+    ws_bytes = int(_L.tt_batched_decode_workspace_bytes(seqs, n, Hq, Hkv, D, kgs))
+    if ws_bytes == 0:
+        _lib.check(_lib.TT_ERR_INVALID_ARGUMENT, "fused_attention_decode_batched")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    raw = np.frombuffer(bytes(seqs), dtype=np.uint8)
+    seqs_dev = torch.from_numpy(raw.copy()).cuda()
+    rc = _L.tt_fused_attention_decode_batched(seqs, seqs_dev.data_ptr(), n, Hq, Hkv, D, kgs, int(fp16), ws.data_ptr(),
+                                              ws_bytes, _stream())
+    _lib.check(rc, "fused_attention_decode_batched")
+    st.finish()
+
+
 def quantize_k_block(K, packed, scale, zero, num_heads, head_dim, k_group_size=16, pbs_metadata_dtype="fp32"):
     """2-bit per-channel quantisation of one K block (bindings.cpp:180-212)."""
     H, D, kgs = int(num_heads), int(head_dim), int(k_group_size)

@@ -24,6 +24,19 @@ _i = C.c_int
 _f = C.c_float
 _sz = C.c_size_t
 
+
+
+class DecodeSeq(C.Structure):
+    """tt_decode_seq: one sequence of a batched decode step (device pointers)."""
+    _fields_ = [
+        ("Q", _vp), ("dense_K", _vp), ("dense_V", _vp),
+        ("PBS_K_Packed", _vp), ("PBS_K_Scales", _vp), ("PBS_K_Zeroes", _vp),
+        ("PBS_V_Packed", _vp), ("PBS_V_Scales", _vp), ("PBS_V_Zeroes", _vp),
+        ("PBS_token_ids", _vp), ("attn_output", _vp), ("mean_attn_weights", _vp),
+        ("dense_count", C.c_int32), ("num_blocks", C.c_int32),
+    ]
+
+
 # name -> (restype, argtypes); mirrors include/tritiercache_amd.h
 _SIGNATURES = {
     "tt_last_error": (C.c_char_p, []),
@@ -42,6 +55,8 @@ _SIGNATURES = {
     "tt_attention_partials": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
                                    _i, _vp, _sz, _vp]),
     "tt_attention_finalize": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "tt_batched_decode_workspace_bytes": (_sz, [C.POINTER(DecodeSeq), _i, _i, _i, _i, _i]),
+    "tt_fused_attention_decode_batched": (_i, [C.POINTER(DecodeSeq), _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "tt_engine_create": (_i, [C.POINTER(_vp), _i, _i, _i, _i, _i, _i, _f, _f, _i, _i, C.c_char_p, _vp]),
     "tt_engine_destroy": (_i, [_vp]),
     "tt_engine_step": (_i, [_vp, _vp, _vp, _vp, _vp, _vp]),

@@ -82,4 +82,32 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
 // Validates shapes the kernels support.
 int attn_check_shapes(int Hq, int Hkv, int D, int kgs);
 
+// Whether head_dim D runs on the matrix-core split kernel (and the batched one).
+bool use_packed_kernel(int D);
+
+// Batched ragged decode (head_dim 128): sequences per launch; their plan
+// travels in the kernel arguments.
+constexpr int kMaxBatchSeqs = 64;
+
+// Split-K plan of one batched launch over seqs[0, nseq). Every sequence gets
+// partial slots in proportion to its work (packed pairs + FP32 tiles); the
+// slots of all sequences together make one round of resident workgroups.
+// Workspace: part_ml [slot][Hq][2] and part_acc [slot][Hq][128] in per-sequence
+// runs ([Hq][nsplit_i] each), row statistics [nseq][Hq][2], logits [Hq][ld_i]
+// per sequence that wants mean weights.
+struct BatchPlan {
+    int nseq = 0;
+    int total_slots = 0;
+    int slot_base[kMaxBatchSeqs + 1] = {};  // prefix of per-sequence slot counts
+    int tok_base[kMaxBatchSeqs + 1] = {};   // prefix of per-sequence logits row strides
+    int mean_base[kMaxBatchSeqs + 1] = {};  // prefix of per-sequence mean-weight workgroups
+    int nsplit_p[kMaxBatchSeqs] = {};       // packed slots of each sequence (the rest are FP32-tier slots)
+    size_t off_ml = 0, off_acc = 0, off_rowstat = 0, off_logits = 0, bytes = 0;
+};
+
+BatchPlan batch_plan(const tt_decode_seq* seqs, int nseq, int Hq, int Hkv, int D, int kgs, int meta_fp16);
+// Enqueues the batched partials and the batched merge / mean weights.
+int batch_launch(const BatchPlan& plan, const tt_decode_seq* seqs_dev, int Hq, int Hkv, int kgs, int meta_fp16,
+                 void* ws, hipStream_t stream);
+
 }  // namespace tt

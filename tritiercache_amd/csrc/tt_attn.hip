@@ -477,7 +477,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 // the accumulators of splits g, g + groups, ... (up to kMergeU per group and
 // block of 256 splits, all in flight together).
 constexpr int kMergeU = 16;
-__device__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
+__device__ __forceinline__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const float* ml = a.part_ml + static_cast<size_t>(h) * a.nsplit * 2;
@@ -609,7 +609,7 @@ struct FbToken {
 // kMeanTokens tokens each. The loads of a block's feedback ids and scores are
 // issued when the block starts, those of the next block's logits as soon as
 // the current ones are consumed.
-__device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, float* sh) {
+__device__ __forceinline__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, float* sh) {
     const int t = threadIdx.x;
     const int Hq = a.Hq;
     int n = a.n_static;
@@ -747,6 +747,141 @@ __global__ void __launch_bounds__(256) attn_finalize_kernel(FinArgs a) {
         fin_mean_tokens(a, b - a.Hq, static_cast<int>(gridDim.x) - a.Hq, sh);
 }
 
+// ---------------------------------------------------------------------------
+// Batched ragged decode (head_dim 128). One launch of the split kernel covers
+// many sequences: the partial slots of all of them form one global slot
+// range (sequence i owns slots [slot_base[i], slot_base[i + 1])), laid over
+// the grid exactly as attn_packed_kernel lays out one sequence's slots, so
+// the KV heads of one slot still share an XCD. A workgroup finds its sequence
+// by a binary search of the prefix table in the kernel arguments and reads
+// that sequence's tier pointers from the caller's device array.
+
+struct BatchArgs {
+    const tt_decode_seq* __restrict__ seqs;
+    float* ml;
+    float* acc;
+    float* logits;
+    float scale2;
+    int nseq, total_slots, Hq, Hkv, kgs, meta_fp16, hc, chunks;
+    int slot_base[kMaxBatchSeqs + 1];
+    int tok_base[kMaxBatchSeqs + 1];
+    int nsplit_p[kMaxBatchSeqs];
+};
+
+// Largest i < n with base[i] <= x (base non-decreasing, base[0] = 0 <= x).
+__device__ __forceinline__ int batch_find(const int* base, const int n, const int x) {
+    int lo = 0, hi = n;
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (base[mid] <= x)
+            lo = mid;
+        else
+            hi = mid;
+    }
+    return lo;
+}
+
+template <int GP, typename MetaT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GP == 8 ? 3 : 1)))
+attn_batched_kernel(const BatchArgs b) {
+    constexpr int kLds = MfLds<GP>::TOTAL > DnLds<GP>::TOTAL ? MfLds<GP>::TOTAL : DnLds<GP>::TOTAL;
+    __shared__ __align__(16) char lds[kLds];
+    const unsigned id = blockIdx.x;
+    const unsigned q = id >> 3;
+    const int hz = static_cast<int>(q % static_cast<unsigned>(b.hc));
+    const int g = static_cast<int>((q / static_cast<unsigned>(b.hc)) * 8 + (id & 7));
+    if (g >= b.total_slots) return;  // padding slot of the last group of 8
+    const int i = batch_find(b.slot_base, b.nseq, g);
+    const int s = g - b.slot_base[i];
+    const tt_decode_seq& d = b.seqs[i];
+    SplitArgs a;
+    a.in.Q = d.Q;
+    a.in.k0 = d.dense_K;
+    a.in.v0 = d.dense_V;
+    a.in.n0 = d.dense_count;
+    a.in.kp = d.PBS_K_Packed;
+    a.in.ks = d.PBS_K_Scales;
+    a.in.kz = d.PBS_K_Zeroes;
+    a.in.vp = d.PBS_V_Packed;
+    a.in.vs = d.PBS_V_Scales;
+    a.in.vz = d.PBS_V_Zeroes;
+    a.in.ids = d.PBS_token_ids;
+    a.in.num_blocks = d.num_blocks;
+    a.in.Hq = b.Hq;
+    a.in.Hkv = b.Hkv;
+    a.in.D = kMfD;
+    a.in.kgs = b.kgs;
+    a.in.meta_fp16 = b.meta_fp16;
+    a.scale2 = b.scale2;
+    a.part_ml = b.ml + static_cast<size_t>(b.slot_base[i]) * b.Hq * 2;
+    a.part_acc = b.acc + static_cast<size_t>(b.slot_base[i]) * b.Hq * kMfD;
+    a.logits = d.mean_attn_weights ? b.logits + static_cast<size_t>(b.tok_base[i]) * b.Hq : nullptr;
+    a.ld = b.tok_base[i + 1] - b.tok_base[i];
+    a.nsplit = b.slot_base[i + 1] - b.slot_base[i];
+    a.nsplit_p = b.nsplit_p[i];
+    a.nsplit_d = a.nsplit - a.nsplit_p;
+    a.wd = 8;
+    a.wp = 1;
+    const int kvh = hz / b.chunks, chunk = hz - kvh * b.chunks;
+    if (s >= a.nsplit_p) {
+        dense_body<GP>(a, s - a.nsplit_p, kvh, chunk, lds);
+        return;
+    }
+    packed_body<GP, MetaT>(a, s, kvh, chunk, lds);
+}
+
+struct FinBatchArgs {
+    const tt_decode_seq* __restrict__ seqs;
+    const float* ml;
+    const float* acc;
+    const float* logits;
+    float* rowstat;
+    int nseq, Hq, kgs;
+    int slot_base[kMaxBatchSeqs + 1];
+    int tok_base[kMaxBatchSeqs + 1];
+    int mean_base[kMaxBatchSeqs + 1];
+};
+
+__device__ __forceinline__ FinArgs fin_batch_args(const FinBatchArgs& b, const int i) {
+    const tt_decode_seq& d = b.seqs[i];
+    FinArgs a;
+    a.part_ml = b.ml + static_cast<size_t>(b.slot_base[i]) * b.Hq * 2;
+    a.part_acc = b.acc + static_cast<size_t>(b.slot_base[i]) * b.Hq * kMfD;
+    a.nsplit = b.slot_base[i + 1] - b.slot_base[i];
+    a.D = kMfD;
+    a.Hq = b.Hq;
+    a.out = d.attn_output;
+    a.rowstat = b.rowstat + static_cast<size_t>(i) * 2 * b.Hq;
+    a.logits = d.mean_attn_weights ? b.logits + static_cast<size_t>(b.tok_base[i]) * b.Hq : nullptr;
+    a.ld = b.tok_base[i + 1] - b.tok_base[i];
+    a.n_static = d.dense_count + d.num_blocks * b.kgs;
+    a.state = nullptr;
+    a.kgs = b.kgs;
+    a.mw = d.mean_attn_weights;
+    a.head_w = nullptr;
+    a.head_w_ld = 0;
+    a.fb = Feedback{};
+    return a;
+}
+
+// Workgroups [0, nseq Hq): the merge of (sequence, query head); the rest:
+// mean weights, sequence i owning [mean_base[i], mean_base[i + 1]).
+__global__ void __launch_bounds__(256) attn_finalize_batched_kernel(const FinBatchArgs b) {
+    extern __shared__ float sh[];
+    const int blk = static_cast<int>(blockIdx.x);
+    const int merges = b.nseq * b.Hq;
+    if (blk < merges) {
+        const int i = blk / b.Hq;
+        const FinArgs a = fin_batch_args(b, i);
+        fin_merge_head(a, blk - i * b.Hq, sh);
+        return;
+    }
+    const int m = blk - merges;
+    const int i = batch_find(b.mean_base, b.nseq, m);
+    const FinArgs a = fin_batch_args(b, i);
+    fin_mean_tokens(a, m - b.mean_base[i], b.mean_base[i + 1] - b.mean_base[i], sh);
+}
+
 template <int CPL, int GP>
 int launch_split_meta(const SplitArgs& a, dim3 grid, int meta_fp16, hipStream_t st) {
     if (meta_fp16)
@@ -792,12 +927,20 @@ int launch_packed(const SplitArgs& a, int Hkv, int chunks, int gp, int meta_fp16
     }
 }
 
+template <int GP>
+int launch_batched_meta(const BatchArgs& b, unsigned wgs, int meta_fp16, hipStream_t st) {
+    if (meta_fp16)
+        hipLaunchKernelGGL((attn_batched_kernel<GP, uint16_t>), dim3(wgs), dim3(256), 0, st, b);
+    else
+        hipLaunchKernelGGL((attn_batched_kernel<GP, float>), dim3(wgs), dim3(256), 0, st, b);
+    TT_LAUNCH_CHECK();
+    return TT_OK;
+}
+
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
 
 int gp_for(int G) { return G >= 8 ? 8 : (G > 4 ? 8 : (G > 2 ? 4 : G)); }
 
-// The matrix-core path serves head_dim 128 with either block size.
-bool use_packed_kernel(int D) { return D == kMfD; }
 
 template <typename MetaT>
 const void* packed_kernel_ptr(int gp) {
@@ -864,6 +1007,9 @@ Residency split_residency(int D, int G, int fp16) {
 }
 
 }  // namespace
+
+// The matrix-core path serves head_dim 128 with either block size.
+bool use_packed_kernel(int D) { return D == kMfD; }
 
 int attn_check_shapes(int Hq, int Hkv, int D, int kgs) {
     if (Hq <= 0 || Hkv <= 0 || D <= 0)
@@ -1014,6 +1160,122 @@ int attn_launch(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out
     int rc = attn_launch_split(in, plan, ws, stream);
     if (rc != TT_OK) return rc;
     return attn_launch_finalize(in, plan, ws, out, mean_w, fb, head_w, head_w_ld, stream);
+}
+
+BatchPlan batch_plan(const tt_decode_seq* seqs, int nseq, int Hq, int Hkv, int D, int kgs, int meta_fp16) {
+    BatchPlan p;
+    p.nseq = nseq;
+    const int W = kgs / 16;
+    const int G = Hq / Hkv;
+    const int gp = gp_for(G);
+    const long long heads = static_cast<long long>(Hkv) * ((G + gp - 1) / gp);
+    const Residency res = split_residency(D, G, meta_fp16);
+    // Slots per head that fill the device once; fewer when the batch is small
+    // (at least ~8 units of work per slot, as for one sequence).
+    const long long round = std::max<long long>(1, static_cast<long long>(res.cus) * res.per_cu / heads);
+    constexpr long long kDenseTileCost = 4;
+    long long units[kMaxBatchSeqs], dunits[kMaxBatchSeqs], total = 0, mean_blocks = 0;
+    for (int i = 0; i < nseq; ++i) {
+        const long long pairs = (static_cast<long long>(seqs[i].num_blocks) * W + 1) / 2;
+        dunits[i] = (static_cast<long long>(seqs[i].dense_count) + 15) / 16 * kDenseTileCost;
+        units[i] = pairs + dunits[i];
+        total += units[i];
+        if (seqs[i].mean_attn_weights)
+            mean_blocks += (static_cast<long long>(seqs[i].dense_count) + static_cast<long long>(seqs[i].num_blocks) * kgs +
+                            kMeanTokens - 1) / kMeanTokens;
+    }
+    const long long target = std::max<long long>(1, std::min<long long>(round, total / 8));
+    const long long per_wg = std::max<long long>(1, (mean_blocks + kMeanMaxWgs - 1) / kMeanMaxWgs);
+    long long slot = 0, tok = 0, mean = 0;
+    for (int i = 0; i < nseq; ++i) {
+        long long n = total > 0 ? (units[i] * target + total / 2) / total : 1;
+        n = std::max<long long>(1, n);
+        const long long dtiles = dunits[i] / kDenseTileCost;
+        long long nd = 0;
+        if (dtiles > 0) {
+            nd = (n * dunits[i] + units[i] / 2) / units[i];
+            nd = std::max<long long>(1, std::min(nd, dtiles));
+        }
+        const long long np = std::max<long long>(1, n - nd);
+        p.slot_base[i] = static_cast<int>(slot);
+        p.nsplit_p[i] = static_cast<int>(np);
+        slot += np + nd;
+        p.tok_base[i] = static_cast<int>(tok);
+        p.mean_base[i] = static_cast<int>(mean);
+        if (seqs[i].mean_attn_weights) {
+            const long long tub = static_cast<long long>(seqs[i].dense_count) + static_cast<long long>(seqs[i].num_blocks) * kgs;
+            tok += (tub + 3) & ~3LL;
+            mean += ((tub + kMeanTokens - 1) / kMeanTokens + per_wg - 1) / per_wg;
+        }
+    }
+    p.slot_base[nseq] = static_cast<int>(slot);
+    p.tok_base[nseq] = static_cast<int>(tok);
+    p.mean_base[nseq] = static_cast<int>(mean);
+    p.total_slots = static_cast<int>(slot);
+    size_t off = 0;
+    p.off_ml = off;
+    off = align256(off + sizeof(float) * 2 * static_cast<size_t>(Hq) * slot);
+    p.off_acc = off;
+    off = align256(off + sizeof(float) * static_cast<size_t>(Hq) * slot * D);
+    p.off_rowstat = off;
+    off = align256(off + sizeof(float) * 2 * static_cast<size_t>(Hq) * std::max(nseq, 1));
+    p.off_logits = off;
+    off = align256(off + sizeof(float) * static_cast<size_t>(Hq) * std::max<long long>(tok, 4));
+    p.bytes = off;
+    return p;
+}
+
+int batch_launch(const BatchPlan& plan, const tt_decode_seq* seqs_dev, int Hq, int Hkv, int kgs, int meta_fp16,
+                 void* ws, hipStream_t stream) {
+    if (plan.nseq <= 0) return TT_OK;
+    char* base = static_cast<char*>(ws);
+    const int G = Hq / Hkv;
+    const int gp = gp_for(G);
+    const int chunks = (G + gp - 1) / gp;
+    BatchArgs b;
+    b.seqs = seqs_dev;
+    b.ml = reinterpret_cast<float*>(base + plan.off_ml);
+    b.acc = reinterpret_cast<float*>(base + plan.off_acc);
+    b.logits = reinterpret_cast<float*>(base + plan.off_logits);
+    b.scale2 = kLog2e / sqrtf(static_cast<float>(kMfD));
+    b.nseq = plan.nseq;
+    b.total_slots = plan.total_slots;
+    b.Hq = Hq;
+    b.Hkv = Hkv;
+    b.kgs = kgs;
+    b.meta_fp16 = meta_fp16 ? 1 : 0;
+    b.hc = Hkv * chunks;
+    b.chunks = chunks;
+    std::memcpy(b.slot_base, plan.slot_base, sizeof(b.slot_base));
+    std::memcpy(b.tok_base, plan.tok_base, sizeof(b.tok_base));
+    std::memcpy(b.nsplit_p, plan.nsplit_p, sizeof(b.nsplit_p));
+    const long long wgs = static_cast<long long>((plan.total_slots + 7) / 8) * 8 * b.hc;
+    if (wgs > 0x7fffffffLL) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "attention grid too large");
+    int rc = TT_OK;
+    switch (gp) {
+    case 1: rc = launch_batched_meta<1>(b, static_cast<unsigned>(wgs), meta_fp16, stream); break;
+    case 2: rc = launch_batched_meta<2>(b, static_cast<unsigned>(wgs), meta_fp16, stream); break;
+    case 4: rc = launch_batched_meta<4>(b, static_cast<unsigned>(wgs), meta_fp16, stream); break;
+    default: rc = launch_batched_meta<8>(b, static_cast<unsigned>(wgs), meta_fp16, stream); break;
+    }
+    if (rc) return rc;
+    FinBatchArgs f;
+    f.seqs = seqs_dev;
+    f.ml = b.ml;
+    f.acc = b.acc;
+    f.logits = b.logits;
+    f.rowstat = reinterpret_cast<float*>(base + plan.off_rowstat);
+    f.nseq = plan.nseq;
+    f.Hq = Hq;
+    f.kgs = kgs;
+    std::memcpy(f.slot_base, plan.slot_base, sizeof(f.slot_base));
+    std::memcpy(f.tok_base, plan.tok_base, sizeof(f.tok_base));
+    std::memcpy(f.mean_base, plan.mean_base, sizeof(f.mean_base));
+    const size_t lds = sizeof(float) * std::max<size_t>(8 + 4 * 256, 2 * static_cast<size_t>(Hq) + 256 * 4);
+    const long long fwgs = static_cast<long long>(plan.nseq) * Hq + plan.mean_base[plan.nseq];
+    hipLaunchKernelGGL(attn_finalize_batched_kernel, dim3(static_cast<unsigned>(fwgs)), dim3(256), lds, stream, f);
+    TT_LAUNCH_CHECK();
+    return TT_OK;
 }
 
 }  // namespace tt

@@ -111,6 +111,46 @@ int fused_impl(const float* Q, const float* dK, const float* dV, int dense_count
     return attn_launch(in, plan, ws, out, mw, nullptr, nullptr, 0, s);
 }
 
+// Validates a batch: shapes, and each sequence as tt_fused_attention_decode
+// validates its arguments.
+int check_batch(const tt_decode_seq* seqs, int num_seqs, int Hq, int Hkv, int D, int kgs) {
+    if (num_seqs < 0) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_seqs must be non-negative.");
+    if (num_seqs > 0 && !seqs) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'seqs' pointer address is NULL.");
+    int rc = attn_check_shapes(Hq, Hkv, D, kgs);
+    if (rc) return rc;
+    long long tokens = 0;
+    for (int i = 0; i < num_seqs; ++i) {
+        const tt_decode_seq& q = seqs[i];
+        tokens += static_cast<long long>(q.dense_count) + static_cast<long long>(q.num_blocks) * kgs + 4;
+        if (tokens > INT_MAX) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "the batch holds more than 2^31 tokens.");
+        AttnInputs in;
+        AttnPlan plan;
+        rc = prepare(q.Q, q.dense_K, q.dense_V, q.dense_count, q.PBS_K_Packed, q.PBS_K_Scales, q.PBS_K_Zeroes,
+                     q.PBS_V_Packed, q.PBS_V_Scales, q.PBS_V_Zeroes, q.PBS_token_ids, q.num_blocks, Hq, Hkv, D, kgs, 0,
+                     false, &in, &plan);
+        if (rc) return rc;
+        if (!q.attn_output) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'attn_output' pointer address is NULL.");
+    }
+    return TT_OK;
+}
+
+// Workspace of a batch: the largest launch (chunks of kMaxBatchSeqs sequences
+// run one after another on the stream and share it); other head dims run the
+// sequences one at a time.
+size_t batch_bytes(const tt_decode_seq* seqs, int num_seqs, int Hq, int Hkv, int D, int kgs, int meta_fp16) {
+    size_t b = 0;
+    if (!use_packed_kernel(D)) {
+        for (int i = 0; i < num_seqs; ++i)
+            b = std::max(b, attn_plan(seqs[i].dense_count, seqs[i].num_blocks, Hq, Hkv, D, kgs,
+                                      seqs[i].mean_attn_weights != nullptr, meta_fp16)
+                                .bytes);
+        return b;
+    }
+    for (int c0 = 0; c0 < num_seqs; c0 += kMaxBatchSeqs)
+        b = std::max(b, batch_plan(seqs + c0, std::min(kMaxBatchSeqs, num_seqs - c0), Hq, Hkv, D, kgs, meta_fp16).bytes);
+    return b;
+}
+
 }  // namespace
 }  // namespace tt
 
@@ -252,6 +292,51 @@ int tt_attention_finalize(const float* Q, int dense_count, int num_blocks, int n
                       static_cast<const int64_t*>(ph), num_blocks, num_q_heads, num_kv_heads, head_dim, attn_output,
                       mean_attn_weights, k_group_size, meta_fp16, workspace, workspace_bytes, false, kFinalize,
                       want_mean_weights, as_stream(stream));
+}
+
+size_t tt_batched_decode_workspace_bytes(const tt_decode_seq* seqs, int num_seqs, int num_q_heads, int num_kv_heads,
+                                         int head_dim, int k_group_size) {
+    clear_error();
+    if (check_batch(seqs, num_seqs, num_q_heads, num_kv_heads, head_dim, k_group_size) != TT_OK) return 0;
+    if (num_seqs == 0) return 256;
+    // The largest plan over both metadata types (their split counts can differ).
+    return std::max(batch_bytes(seqs, num_seqs, num_q_heads, num_kv_heads, head_dim, k_group_size, 0),
+                    batch_bytes(seqs, num_seqs, num_q_heads, num_kv_heads, head_dim, k_group_size, 1));
+}
+
+int tt_fused_attention_decode_batched(const tt_decode_seq* seqs, const tt_decode_seq* seqs_device, int num_seqs,
+                                      int num_q_heads, int num_kv_heads, int head_dim, int k_group_size, int meta_fp16,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+    clear_error();
+    const int Hq = num_q_heads, Hkv = num_kv_heads, D = head_dim, kgs = k_group_size;
+    int rc = check_batch(seqs, num_seqs, Hq, Hkv, D, kgs);
+    if (rc) return rc;
+    if (num_seqs == 0) return TT_OK;
+    if (!workspace || workspace_bytes < batch_bytes(seqs, num_seqs, Hq, Hkv, D, kgs, meta_fp16))
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "workspace is NULL or smaller than tt_batched_decode_workspace_bytes().");
+    const hipStream_t s = as_stream(stream);
+    if (!use_packed_kernel(D)) {
+        for (int i = 0; i < num_seqs; ++i) {
+            const tt_decode_seq& q = seqs[i];
+            AttnInputs in;
+            AttnPlan plan;
+            rc = prepare(q.Q, q.dense_K, q.dense_V, q.dense_count, q.PBS_K_Packed, q.PBS_K_Scales, q.PBS_K_Zeroes,
+                         q.PBS_V_Packed, q.PBS_V_Scales, q.PBS_V_Zeroes, q.PBS_token_ids, q.num_blocks, Hq, Hkv, D, kgs,
+                         meta_fp16, q.mean_attn_weights != nullptr, &in, &plan);
+            if (rc) return rc;
+            rc = attn_launch(in, plan, workspace, q.attn_output, q.mean_attn_weights, nullptr, nullptr, 0, s);
+            if (rc) return rc;
+        }
+        return TT_OK;
+    }
+    if (!seqs_device) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'seqs_device' pointer address is NULL.");
+    for (int c0 = 0; c0 < num_seqs; c0 += kMaxBatchSeqs) {
+        const int n = std::min(kMaxBatchSeqs, num_seqs - c0);
+        const BatchPlan plan = batch_plan(seqs + c0, n, Hq, Hkv, D, kgs, meta_fp16);
+        rc = batch_launch(plan, seqs_device + c0, Hq, Hkv, kgs, meta_fp16, workspace, s);
+        if (rc) return rc;
+    }
+    return TT_OK;
 }
 
 }  // extern "C"
