@@ -477,7 +477,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 // the accumulators of splits g, g + groups, ... (up to kMergeU per group and
 // block of 256 splits, all in flight together).
 constexpr int kMergeU = 16;
-__device__ __forceinline__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
+__device__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const float* ml = a.part_ml + static_cast<size_t>(h) * a.nsplit * 2;
@@ -609,7 +609,7 @@ struct FbToken {
 // kMeanTokens tokens each. The loads of a block's feedback ids and scores are
 // issued when the block starts, those of the next block's logits as soon as
 // the current ones are consumed.
-__device__ __forceinline__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, float* sh) {
+__device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, float* sh) {
     const int t = threadIdx.x;
     const int Hq = a.Hq;
     int n = a.n_static;
