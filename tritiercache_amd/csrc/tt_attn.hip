@@ -650,11 +650,11 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
     // Thread (head group hg, token quad q): heads hg, hg + kMeanGroups, ...;
     // tokens tok0 + 4 q .. + 3. Rows are padded to a multiple of 4 floats.
     const int q = t % kMeanQuads, hg = t / kMeanQuads;
-    float4 lgv[8];
-    fin_load_logits(a, 0, hg, wg * kMeanTokens + 4 * q, n, lgv);
     // (M_h, 1/L_h) of every head: 8 threads per head, splits j0, j0 + 8, ...
     // (every workgroup rebuilds them: a second launch that waits for the
-    // merge costs more than these loads)
+    // merge costs more than these loads). Their loads are issued first: they
+    // are on the critical path, the first block's logits load (issued next)
+    // is not.
     float* Mh = sh;        // [Hq]
     float* iL = sh + Hq;   // [Hq]
     for (int h0 = 0; h0 < Hq; h0 += 32) {
@@ -662,30 +662,33 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
         const float* ml = a.part_ml + static_cast<size_t>(h < Hq ? h : 0) * a.nsplit * 2;
         float mx = kNegInf, ls = 0.0f;
         for (int jb = j0; jb < a.nsplit; jb += 8 * kMergeU) {
-            float mv[kMergeU], lv[kMergeU];
+            float2 v[kMergeU];  // (m, l) of split jb + 8 u
 #pragma unroll
             for (int u = 0; u < kMergeU; ++u) {
                 const int j = jb + 8 * u;
-                mv[u] = j < a.nsplit ? ml[2 * j] : kNegInf;
-                lv[u] = j < a.nsplit ? ml[2 * j + 1] : 0.0f;
+                v[u] = j < a.nsplit ? *reinterpret_cast<const float2*>(ml + 2 * j) : make_float2(kNegInf, 0.0f);
             }
             float bm = kNegInf;
 #pragma unroll
-            for (int u = 0; u < kMergeU; ++u) bm = fmaxf(bm, mv[u]);
+            for (int u = 0; u < kMergeU; ++u) bm = fmaxf(bm, v[u].x);
             const float mn = fmaxf(mx, bm);
             float bs = 0.0f;
+            // hardware exp2: arguments <= 0, results below 2^-126 flush to 0
 #pragma unroll
-            for (int u = 0; u < kMergeU; ++u) bs += (mv[u] == kNegInf) ? 0.0f : exp2f(mv[u] - mn) * lv[u];
-            ls = ((mx == kNegInf) ? 0.0f : ls * exp2f(mx - mn)) + bs;
+            for (int u = 0; u < kMergeU; ++u)
+                bs += (v[u].x == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(v[u].x - mn) * v[u].y;
+            ls = ((mx == kNegInf) ? 0.0f : ls * __builtin_amdgcn_exp2f(mx - mn)) + bs;
             mx = mn;
         }
         const float gm = max8(mx);
-        const float gl = sum8((mx == kNegInf) ? 0.0f : ls * exp2f(mx - gm));
+        const float gl = sum8((mx == kNegInf) ? 0.0f : ls * __builtin_amdgcn_exp2f(mx - gm));
         if (j0 == 0 && h < Hq) {
             Mh[h] = gm;
             iL[h] = 1.0f / (gl > 0.0f ? gl : 1.0f);
         }
     }
+    float4 lgv[8];
+    fin_load_logits(a, 0, hg, wg * kMeanTokens + 4 * q, n, lgv);
     __syncthreads();
     float* red = sh + 2 * Hq;  // [kMeanGroups][kMeanTokens]
     for (int blk = wg; blk * kMeanTokens < n; blk += nwg) {
