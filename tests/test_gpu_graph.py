@@ -120,3 +120,76 @@ def test_quantizers_graph_replays(lib, oracle):
             assert same_bits(host(kp[b:b + 1]), p) and same_bits(host(ks[b]), s) and same_bits(host(kz[b]), z), rep
         p, s, z = oracle.quantize_v(Vh, False)
         assert same_bits(host(vp), p) and same_bits(host(vs), s) and same_bits(host(vz), z), rep
+
+
+def test_batched_decode_graph_replays(lib, oracle):
+    """tt_fused_attention_decode_batched captured once (its plan is fixed at capture) and replayed with new queries:
+    every replay equals an eager call bit for bit and matches the oracle per sequence."""
+    L = lib.load()
+    Hq, Hkv, D, kgs = 32, 8, 128, 16
+    sizes = [(260, 40), (0, 25), (300, 0), (17, 3), (120, 90)]
+    cases = [K.make_case(oracle, Hq, Hkv, D, nd, nb, kgs, False, "tail", seed=1500 + i) for i, (nd, nb) in enumerate(sizes)]
+    keep = []
+
+    def tensors(args):
+        (Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, *_rest) = args
+        return {k: dev(v) for k, v in dict(Q=Q, dK=dK, dV=dV, KP=KP, KS=KS, KZ=KZ, VP=VP, VS=VS, VZ=VZ, ids=ids).items()}
+
+    ts = [tensors(a) for a in cases]
+
+    def descs(outs, mws):
+        arr = (lib.DecodeSeq * len(cases))()
+        for i, (a, t) in enumerate(zip(cases, ts)):
+            nd, nb = a[3], a[11]
+            s = arr[i]
+            s.Q = t["Q"].data_ptr()
+            if nd:
+                s.dense_K, s.dense_V = t["dK"].data_ptr(), t["dV"].data_ptr()
+            if nb:
+                s.PBS_K_Packed, s.PBS_K_Scales, s.PBS_K_Zeroes = (t["KP"].data_ptr(), t["KS"].data_ptr(),
+                                                                  t["KZ"].data_ptr())
+                s.PBS_V_Packed, s.PBS_V_Scales, s.PBS_V_Zeroes = (t["VP"].data_ptr(), t["VS"].data_ptr(),
+                                                                  t["VZ"].data_ptr())
+                s.PBS_token_ids = t["ids"].data_ptr()
+            s.attn_output, s.mean_attn_weights = outs[i].data_ptr(), mws[i].data_ptr()
+            s.dense_count, s.num_blocks = nd, nb
+        d = torch.from_numpy(np.frombuffer(bytes(arr), dtype=np.uint8).copy()).cuda()
+        keep.append(d)
+        return arr, d
+
+    g_out = [torch.zeros((Hq, D), device="cuda") for _ in cases]
+    g_mw = [torch.zeros((a[3] + a[11] * kgs,), device="cuda") for a in cases]
+    e_out = [torch.zeros_like(x) for x in g_out]
+    e_mw = [torch.zeros_like(x) for x in g_mw]
+    g_arr, g_dev = descs(g_out, g_mw)
+    e_arr, e_dev = descs(e_out, e_mw)
+    n = len(cases)
+    ws_bytes = int(L.tt_batched_decode_workspace_bytes(g_arr, n, Hq, Hkv, D, kgs))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    e_ws = torch.empty_like(ws)
+
+    def call(arr, d, work):
+        lib.check(L.tt_fused_attention_decode_batched(arr, d.data_ptr(), n, Hq, Hkv, D, kgs, 0, work.data_ptr(),
+                                                      ws_bytes, _stream()), "batched")
+
+    call(g_arr, g_dev, ws)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call(g_arr, g_dev, ws)
+    for rep in range(3):
+        for i, t in enumerate(ts):
+            t["Q"].copy_(dev(synth.normal(7100 + 10 * rep + i, 0, (Hq, D))))
+        for x in g_out + g_mw:
+            x.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        call(e_arr, e_dev, e_ws)
+        torch.cuda.synchronize()
+        for i, a in enumerate(cases):
+            assert torch.equal(g_out[i], e_out[i]), (rep, i)
+            assert torch.equal(g_mw[i], e_mw[i]), (rep, i)
+            hargs = (host(ts[i]["Q"]),) + tuple(a[1:])
+            ro, rmw = oracle.fused_attention_decode(*hargs)
+            assert rel_err(host(g_out[i]), ro) <= K.ATTN_TOL, (rep, i)
+            assert rel_err(host(g_mw[i]), rmw) <= K.ATTN_TOL, (rep, i)
