@@ -59,7 +59,8 @@ def _compare_state(g, o, tag):
         assert same_bits(g[name], o[name].reshape(-1)), (tag, name)
 
 
-@pytest.mark.parametrize("run", ["step_small_fp16", "step_prefill_kgs32_fp32", "step_gqa_d128_fp32"])
+@pytest.mark.parametrize("run", ["step_small_fp16", "step_prefill_kgs32_fp32", "step_gqa_d128_fp32",
+                                 "step_long_prefill_fp32"])
 def test_full_steps_lockstep_with_oracle(C, oracle, run):
     cfg = engine_runs.RUNS[run]
     eng = gpu_engine(C, cfg)

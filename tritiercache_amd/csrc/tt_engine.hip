@@ -125,6 +125,90 @@ __global__ void __launch_bounds__(1024) threshold_kernel(const float* __restrict
     }
 }
 
+// The same selection spread over many workgroups: per pass, thr_hist_kernel
+// adds the digit histogram of the candidates that match the prefix found so
+// far into a global histogram (LDS histogram per workgroup, then one atomic
+// per non-empty bin), and thr_select_kernel (one workgroup) finds the digit
+// where the running count passes k, narrows prefix / mask / k, clears the
+// histogram for the next pass and, after the last pass, writes the threshold.
+// Selection state (`ts`): hist[2048], then prefix, mask, k; all zero between
+// selections (the last pass leaves them so).
+constexpr int kThrHistWgs = 64;   // at most, each 256 threads x kThrHistPer candidates per round
+constexpr int kThrHistPer = 16;
+constexpr int kThrStateWords = 2048 + 4;
+// Candidate counts from which the six launches of the spread selection beat
+// the single-workgroup kernel.
+#ifndef TT_THR_MULTI_MIN
+#define TT_THR_MULTI_MIN 16384
+#endif
+constexpr size_t kThrMultiMin = TT_THR_MULTI_MIN;
+
+__device__ __forceinline__ int thr_bits(int pass) { return pass < 2 ? 11 : 10; }
+__device__ __forceinline__ int thr_shift(int pass) { return pass == 0 ? 21 : (pass == 1 ? 10 : 0); }
+
+__global__ void __launch_bounds__(256) thr_hist_kernel(const float* __restrict__ g, int n, int pass,
+                                                       unsigned int* ts) {
+    __shared__ unsigned int hist[2048];
+    const int tid = threadIdx.x;
+    for (int i = tid; i < 2048; i += 256) hist[i] = 0;
+    __syncthreads();
+    const int shift = thr_shift(pass);
+    const unsigned int dm = (1u << thr_bits(pass)) - 1u;
+    const unsigned int prefix = ts[2048], mask = ts[2049];
+    const int stride = gridDim.x * 256 * kThrHistPer;
+    for (int base = blockIdx.x * 256 * kThrHistPer; base < n; base += stride) {
+        unsigned int u[kThrHistPer];
+#pragma unroll
+        for (int j = 0; j < kThrHistPer; ++j) {
+            const int i = base + j * 256 + tid;
+            u[j] = i < n ? __float_as_uint(g[i]) : 0u;
+        }
+#pragma unroll
+        for (int j = 0; j < kThrHistPer; ++j) {
+            const unsigned int key = (u[j] & 0x80000000u) ? ~u[j] : (u[j] | 0x80000000u);
+            if (base + j * 256 + tid < n && (key & mask) == prefix) atomicAdd(&hist[(key >> shift) & dm], 1u);
+        }
+    }
+    __syncthreads();
+    for (int i = tid; i < 2048; i += 256)
+        if (hist[i]) atomicAdd(&ts[i], hist[i]);
+}
+
+__global__ void __launch_bounds__(1024) thr_select_kernel(int pass, long long k0, unsigned int* ts, int* st,
+                                                          int total) {
+    __shared__ unsigned int wtot[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int shift = thr_shift(pass);
+    const unsigned int dm = (1u << thr_bits(pass)) - 1u;
+    const unsigned int prefix = ts[2048], mask = ts[2049];
+    const unsigned int kk = pass == 0 ? static_cast<unsigned int>(k0) : ts[2050];  // k < n < 2^31
+    // Thread t owns bins 2t and 2t + 1 (read, then cleared for the next pass).
+    const unsigned int h0 = ts[2 * tid], h1 = ts[2 * tid + 1];
+    ts[2 * tid] = 0;
+    ts[2 * tid + 1] = 0;
+    const unsigned int incl = wave_incl_scan(h0 + h1);
+    if (lane == 63) wtot[wave] = incl;
+    __syncthreads();
+    unsigned int before = incl - (h0 + h1);
+    for (int w = 0; w < wave; ++w) before += wtot[w];
+    if (before <= kk && kk < before + h0 + h1) {  // exactly one thread
+        const unsigned int d = (kk < before + h0) ? 2u * tid : 2u * tid + 1u;
+        const unsigned int np = prefix | (d << shift);
+        if (pass == 2) {
+            const unsigned int u = (np & 0x80000000u) ? (np & 0x7fffffffu) : ~np;
+            st[kThreshold] = static_cast<int>(u);
+            st[kLastCalcPos] = total;
+            ts[2048] = 0;
+            ts[2049] = 0;
+            ts[2050] = 0;
+        } else {
+            ts[2048] = np;
+            ts[2049] = mask | (dm << shift);
+            ts[2050] = kk - before - (d & 1u ? h0 : 0u);
+        }
+    }
+}
+
 struct RouteArgs {
     int* st;
     const float* k_new;
@@ -451,6 +535,7 @@ struct tt_engine {
     void *PBS_KS = nullptr, *PBS_KZ = nullptr, *PBS_VS = nullptr, *PBS_VZ = nullptr;
     int cap_blocks = 0;
     int* st = nullptr;
+    unsigned int* ts = nullptr;  // threshold selection state (kThrStateWords)
     // host mirror of the data-independent counters
     int h_s = 0, h_rw = 0, h_head = 0, h_total = 0, h_ev = 0, h_last = -1;
     // Heavy hitters grow by at most one per routed eviction (prefill routes
@@ -483,9 +568,16 @@ int engine_free_pbs(tt_engine* e) {
 
 int engine_reserve_ws(tt_engine* e, const AttnPlan& p, hipStream_t s);
 
+constexpr int kLogicalSlack = 64;
+
 // Physical packed-store capacity. Buffers are reallocated (and copied) only
-// when the upper bound on used blocks exceeds the allocation.
+// when the upper bound on used blocks, plus the logical allocation's slack,
+// exceeds the allocation.
 int engine_reserve_blocks(tt_engine* e, int need, hipStream_t s) {
+    // The reference's logical allocation (pbs_allocated_blocks, which sizes the
+    // PBS getters) runs up to kLogicalSlack - 1 blocks past the used count
+    // (cache_engine.cpp:84-116: +64 at a time); the store covers it.
+    need += kLogicalSlack;
     if (need <= e->cap_blocks) return TT_OK;
     const int nc = std::max(need, e->cap_blocks + std::max(64, e->cap_blocks / 2));
     const size_t kvs = e->kvs, ch = e->chunk, msz = e->msz(), W = e->kgs / 16;
@@ -653,7 +745,8 @@ int tt_engine_create(tt_engine** out, int num_q_heads, int num_kv_heads, int hea
         (rc = dev_alloc(&e->HH_scores, e->max_hh)) || (rc = dev_alloc(&e->HH_ids, e->max_hh)) ||
         (rc = dev_alloc(&e->WR_K, e->chunk * kvs)) || (rc = dev_alloc(&e->WR_V, e->chunk * kvs)) ||
         (rc = dev_alloc(&e->WR_ids, e->chunk)) || (rc = dev_alloc(&e->EV_K, kvs)) || (rc = dev_alloc(&e->EV_V, kvs)) ||
-        (rc = dev_alloc(&e->g, e->msl)) || (rc = dev_alloc(&e->st, kStateSlots))) {
+        (rc = dev_alloc(&e->g, e->msl)) || (rc = dev_alloc(&e->st, kStateSlots)) ||
+        (rc = dev_alloc(&e->ts, kThrStateWords))) {
         tt_engine_destroy(e);
         return rc;
     }
@@ -667,6 +760,7 @@ int tt_engine_create(tt_engine** out, int num_q_heads, int num_kv_heads, int hea
     TT_HIP_CHECK(hipMemsetAsync(e->HH_scores, 0, e->max_hh * 4, s));
     TT_HIP_CHECK(hipMemsetAsync(e->WR_K, 0, e->chunk * kvs * 4, s));
     TT_HIP_CHECK(hipMemsetAsync(e->WR_V, 0, e->chunk * kvs * 4, s));
+    TT_HIP_CHECK(hipMemsetAsync(e->ts, 0, kThrStateWords * sizeof(unsigned int), s));
     const int want_blocks = (e->msl + e->chunk - 1) / e->chunk + 1;
     if ((rc = engine_reserve_blocks(e, want_blocks, s))) {
         tt_engine_destroy(e);
@@ -691,6 +785,7 @@ int tt_engine_destroy(tt_engine* e) {
     (void)hipFree(e->HH_ids);
     (void)hipFree(e->WR_ids);
     (void)hipFree(e->st);
+    (void)hipFree(e->ts);
     (void)hipFree(e->ws);
     engine_free_pbs(e);
     if (e->host_state) (void)hipHostFree(e->host_state);
@@ -729,9 +824,22 @@ int tt_engine_ingest(tt_engine* e, const float* K_new, const float* V_new, void*
             if (q < 0.0f) q = 0.0f;
             if (q > 1.0f) q = 1.0f;
             const size_t k = static_cast<size_t>(q * static_cast<float>(n - 1));
-            hipLaunchKernelGGL(threshold_kernel, dim3(1), dim3(1024), 0, s, e->g + cs, static_cast<int>(n),
-                               static_cast<long long>(k), e->st, e->h_total);
-            TT_LAUNCH_CHECK();
+            if (n < kThrMultiMin) {
+                hipLaunchKernelGGL(threshold_kernel, dim3(1), dim3(1024), 0, s, e->g + cs, static_cast<int>(n),
+                                   static_cast<long long>(k), e->st, e->h_total);
+                TT_LAUNCH_CHECK();
+            } else {
+                const int per = 256 * kThrHistPer;
+                const int wgs = static_cast<int>(std::min<size_t>(kThrHistWgs, (n + per - 1) / per));
+                for (int pass = 0; pass < 3; ++pass) {
+                    hipLaunchKernelGGL(thr_hist_kernel, dim3(wgs), dim3(256), 0, s, e->g + cs, static_cast<int>(n),
+                                       pass, e->ts);
+                    TT_LAUNCH_CHECK();
+                    hipLaunchKernelGGL(thr_select_kernel, dim3(1), dim3(1024), 0, s, pass, static_cast<long long>(k),
+                                       e->ts, e->st, e->h_total);
+                    TT_LAUNCH_CHECK();
+                }
+            }
             e->h_last = e->h_total;
         }
         // A flush may need one more block than the current upper bound.
@@ -978,6 +1086,7 @@ int tt_engine_buffer(tt_engine* e, int which, void** p, int64_t* numel, int* es,
     if (rc) return rc;
     const int64_t kvs = static_cast<int64_t>(e->kvs), nb = e->host_state[kLogicalAlloc], ch = e->chunk;
     const int msz = static_cast<int>(e->msz());
+    if (nb > e->cap_blocks) TT_FAIL(TT_ERR_RUNTIME, "packed store smaller than its logical allocation.");
     switch (which) {
     case 0: *p = e->S_K; *numel = e->S * kvs; *es = 4; break;
     case 1: *p = e->S_V; *numel = e->S * kvs; *es = 4; break;
