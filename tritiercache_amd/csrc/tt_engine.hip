@@ -240,6 +240,7 @@ struct RouteArgs {
 };
 
 enum RouteCase : int { kToHH = 0, kReplace = 1, kToWR = 2 };
+constexpr int kRouteRegs = 8;  // row elements per thread kept in registers by the route kernel
 
 template <typename MetaT>
 __device__ void flush_waiting_room(const RouteArgs& a, int blocks) {
@@ -282,15 +283,50 @@ __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
     const int wr = st[kWrCount];
 
     // Evicted row out of the ring slot, new token in (each thread owns the
-    // same elements for the read and the write).
+    // same elements for the read and the write). Rows of up to
+    // 1024 kRouteRegs elements stay in registers until they are written to
+    // their tier; longer rows go through the EV buffers.
     float* rk = a.rw_k + static_cast<size_t>(a.slot) * kvs;
     float* rv = a.rw_v + static_cast<size_t>(a.slot) * kvs;
-    for (int e = tid; e < kvs; e += blockDim.x) {
-        a.ev_k[e] = rk[e];
-        a.ev_v[e] = rv[e];
-        rk[e] = a.k_new[e];
-        rv[e] = a.v_new[e];
+    const bool in_regs = kvs <= 1024 * kRouteRegs;
+    float evk[kRouteRegs], evv[kRouteRegs];
+    if (in_regs) {
+#pragma unroll
+        for (int j = 0; j < kRouteRegs; ++j) {
+            const int e = tid + 1024 * j;
+            if (e < kvs) {
+                evk[j] = rk[e];
+                evv[j] = rv[e];
+                rk[e] = a.k_new[e];
+                rv[e] = a.v_new[e];
+            }
+        }
+    } else {
+        for (int e = tid; e < kvs; e += blockDim.x) {
+            a.ev_k[e] = rk[e];
+            a.ev_v[e] = rv[e];
+            rk[e] = a.k_new[e];
+            rv[e] = a.v_new[e];
+        }
     }
+    // The evicted row into `dk` / `dv` (row layout [kvs]).
+    auto put_evicted = [&](float* dk, float* dv) {
+        if (in_regs) {
+#pragma unroll
+            for (int j = 0; j < kRouteRegs; ++j) {
+                const int e = tid + 1024 * j;
+                if (e < kvs) {
+                    dk[e] = evk[j];
+                    dv[e] = evv[j];
+                }
+            }
+        } else {
+            for (int e = tid; e < kvs; e += blockDim.x) {
+                dk[e] = a.ev_k[e];
+                dv[e] = a.ev_v[e];
+            }
+        }
+    };
 
     // Score and threshold (cache_engine.cpp:216-218).
     const long long eid = a.evicted_id;
@@ -358,12 +394,7 @@ __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
     const int mi = s_min_idx;
 
     if (c == kToHH) {
-        float* hk = a.hh_k + static_cast<size_t>(hh) * kvs;
-        float* hv = a.hh_v + static_cast<size_t>(hh) * kvs;
-        for (int e = tid; e < kvs; e += blockDim.x) {
-            hk[e] = a.ev_k[e];
-            hv[e] = a.ev_v[e];
-        }
+        put_evicted(a.hh_k + static_cast<size_t>(hh) * kvs, a.hh_v + static_cast<size_t>(hh) * kvs);
         if (tid == 0) {
             a.hh_ids[hh] = eid;
             a.hh_scores[hh] = s_score;
@@ -376,21 +407,15 @@ __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
         for (int e = tid; e < kvs; e += blockDim.x) {
             wk[e] = hk[e];
             wv[e] = hv[e];
-            hk[e] = a.ev_k[e];
-            hv[e] = a.ev_v[e];
         }
+        put_evicted(hk, hv);  // each thread overwrites only elements it has read
         if (tid == 0) {
             a.wr_ids[wr] = a.hh_ids[mi];
             a.hh_ids[mi] = eid;
             a.hh_scores[mi] = s_score;
         }
     } else {
-        float* wk = a.wr_k + static_cast<size_t>(wr) * kvs;
-        float* wv = a.wr_v + static_cast<size_t>(wr) * kvs;
-        for (int e = tid; e < kvs; e += blockDim.x) {
-            wk[e] = a.ev_k[e];
-            wv[e] = a.ev_v[e];
-        }
+        put_evicted(a.wr_k + static_cast<size_t>(wr) * kvs, a.wr_v + static_cast<size_t>(wr) * kvs);
         if (tid == 0) a.wr_ids[wr] = eid;
     }
     const int new_hh = hh + (c == kToHH ? 1 : 0);
