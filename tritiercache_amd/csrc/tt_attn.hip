@@ -426,7 +426,7 @@ attn_packed_kernel(SplitArgs a, const int hc, const int chunks) {
 //   [0, Hq)        merge the split partials of query head h (log2 units):
 //                  M = max_j m_j, L = sum_j l_j 2^(m_j - M),
 //                  out = sum_j acc_j 2^(m_j - M) / L.
-//   [Hq, ...)      mean attention weights of kMeanTokens tokens each
+//   [Hq, ...)      mean attention weights of blocks of kMeanTokens (long contexts: kMeanTokensLong) tokens
 //                  (fused_attn_avx2.cpp:286-300): every such workgroup first
 //                  rebuilds (M, 1/L) of all heads from the (m, l) partials,
 //                  then w_h = 2^(s_h - M_h) / L_h summed over the heads and
@@ -565,9 +565,11 @@ __device__ __forceinline__ float sum8(float x) {
 #ifndef TT_MEAN_TOKENS
 #define TT_MEAN_TOKENS 64
 #endif
-constexpr int kMeanTokens = TT_MEAN_TOKENS;  // tokens per mean-weight workgroup
-constexpr int kMeanQuads = kMeanTokens / 4;  // token quads per workgroup
-constexpr int kMeanGroups = 256 / kMeanQuads;  // head groups per workgroup
+constexpr int kMeanTokens = TT_MEAN_TOKENS;  // tokens per mean-weight block
+// Long contexts use blocks twice as long: half the workgroups rebuild the
+// split statistics, and each still has 4 tokens per thread.
+constexpr int kMeanTokensLong = 2 * kMeanTokens;
+constexpr int kMeanLongFrom = 65536;  // attended tokens (upper bound) from which the long blocks pay
 // Mean-weight workgroups at most; past that each takes an equal number of
 // token blocks, so fewer of them rebuild the per-head row statistics.
 #ifndef TT_MEAN_WGS
@@ -575,15 +577,17 @@ constexpr int kMeanGroups = 256 / kMeanQuads;  // head groups per workgroup
 #endif
 constexpr int kMeanMaxWgs = TT_MEAN_WGS;
 
-// Logits of token quad i0 for the heads hb + hg + kMeanGroups u, u < 8
-// (-inf past the end and for missing heads).
+// Logits of token quad i0 for the heads hb + hg + groups u, u < 8 (-inf past
+// the end and for missing heads); groups = head groups of a MT-token block.
+template <int MT>
 __device__ __forceinline__ void fin_load_logits(const FinArgs& a, const int hb, const int hg, const int i0,
                                                 const int n, float4 (&lgv)[8]) {
+    constexpr int kGroups = 256 / (MT / 4);
     const int Hq = a.Hq;
     const bool whole = i0 + 4 <= n;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-        const int h = hb + hg + kMeanGroups * u;
+        const int h = hb + hg + kGroups * u;
         lgv[u] = make_float4(kNegInf, kNegInf, kNegInf, kNegInf);
         if (h < Hq && i0 < n) {
             const float* lg = a.logits + static_cast<size_t>(h) * a.ld + i0;
@@ -606,10 +610,13 @@ struct FbToken {
 };
 
 // Mean-weight workgroup `wg` of `nwg`: token blocks wg, wg + nwg, ... of
-// kMeanTokens tokens each. The loads of a block's feedback ids and scores are
+// MT tokens each. The loads of a block's feedback ids and scores are
 // issued when the block starts, those of the next block's logits as soon as
 // the current ones are consumed.
+template <int MT>
 __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, float* sh) {
+    constexpr int kQuads = MT / 4;         // token quads per block
+    constexpr int kGroups = 256 / kQuads;  // head groups per workgroup
     const int t = threadIdx.x;
     const int Hq = a.Hq;
     int n = a.n_static;
@@ -622,8 +629,8 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
         Nd = s + hh + rw;
         n = Nd + a.state[kBlocksUsed] * a.kgs;
     }
-    if (wg * kMeanTokens >= n) return;
-    // Feedback target of token i (threads t < kMeanTokens, one token each).
+    if (wg * MT >= n) return;
+    // Feedback target of token i (threads t < MT, one token each).
     auto fb_token = [&](const int i) {
         FbToken f{-1, -1};
         if (i >= n) return f;
@@ -640,16 +647,16 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
         if (f.tid < 0 || f.tid >= a.fb.max_seq_len) f.tid = -1;
         return f;
     };
-    const bool fb_lane = a.fb.g && t < kMeanTokens;
+    const bool fb_lane = a.fb.g && t < MT;
     FbToken ft{-1, -1};
     float g_old = 0.0f;
     if (fb_lane) {
-        ft = fb_token(wg * kMeanTokens + t);
+        ft = fb_token(wg * MT + t);
         if (ft.tid >= 0) g_old = a.fb.g[ft.tid];
     }
-    // Thread (head group hg, token quad q): heads hg, hg + kMeanGroups, ...;
+    // Thread (head group hg, token quad q): heads hg, hg + kGroups, ...;
     // tokens tok0 + 4 q .. + 3. Rows are padded to a multiple of 4 floats.
-    const int q = t % kMeanQuads, hg = t / kMeanQuads;
+    const int q = t % kQuads, hg = t / kQuads;
     // (M_h, 1/L_h) of every head: 8 threads per head, splits j0, j0 + 8, ...
     // (every workgroup rebuilds them: a second launch that waits for the
     // merge costs more than these loads). Their loads are issued first: they
@@ -688,11 +695,11 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
         }
     }
     float4 lgv[8];
-    fin_load_logits(a, 0, hg, wg * kMeanTokens + 4 * q, n, lgv);
+    fin_load_logits<MT>(a, 0, hg, wg * MT + 4 * q, n, lgv);
     __syncthreads();
-    float* red = sh + 2 * Hq;  // [kMeanGroups][kMeanTokens]
-    for (int blk = wg; blk * kMeanTokens < n; blk += nwg) {
-        const int tok0 = blk * kMeanTokens;
+    float* red = sh + 2 * Hq;  // [kGroups][MT]
+    for (int blk = wg; blk * MT < n; blk += nwg) {
+        const int tok0 = blk * MT;
         const int i0 = tok0 + 4 * q;
         if (blk != wg && fb_lane) {
             ft = fb_token(tok0 + t);
@@ -700,11 +707,11 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
         }
         float w4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (i0 < n) {
-            for (int hb = 0; hb < Hq; hb += 8 * kMeanGroups) {
-                if (hb > 0) fin_load_logits(a, hb, hg, i0, n, lgv);
+            for (int hb = 0; hb < Hq; hb += 8 * kGroups) {
+                if (hb > 0) fin_load_logits<MT>(a, hb, hg, i0, n, lgv);
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
-                    const int h = hb + hg + kMeanGroups * u;
+                    const int h = hb + hg + kGroups * u;
                     if (h >= Hq) break;
                     const float sc[4] = {lgv[u].x, lgv[u].y, lgv[u].z, lgv[u].w};
                     const float mh = Mh[h], il = iL[h];
@@ -720,15 +727,15 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
             }
         }
         const int nxt = blk + nwg;
-        if (nxt * kMeanTokens < n) fin_load_logits(a, 0, hg, nxt * kMeanTokens + 4 * q, n, lgv);
+        if (nxt * MT < n) fin_load_logits<MT>(a, 0, hg, nxt * MT + 4 * q, n, lgv);
 #pragma unroll
-        for (int e = 0; e < 4; ++e) red[hg * kMeanTokens + 4 * q + e] = w4[e];
+        for (int e = 0; e < 4; ++e) red[hg * MT + 4 * q + e] = w4[e];
         __syncthreads();
         const int i = tok0 + t;
-        if (t < kMeanTokens && i < n) {
+        if (t < MT && i < n) {
             float sum = 0.0f;
 #pragma unroll
-            for (int g = 0; g < kMeanGroups; ++g) sum += red[g * kMeanTokens + t];
+            for (int g = 0; g < kGroups; ++g) sum += red[g * MT + t];
             const float mean = sum / static_cast<float>(Hq);
             if (a.mw) a.mw[i] = mean;
             if (fb_lane && ft.tid >= 0) {
@@ -741,13 +748,14 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
     }
 }
 
+template <int MT>
 __global__ void __launch_bounds__(256) attn_finalize_kernel(FinArgs a) {
     extern __shared__ float sh[];
     const int b = static_cast<int>(blockIdx.x);
     if (b < a.Hq)
         fin_merge_head(a, b, sh);
     else
-        fin_mean_tokens(a, b - a.Hq, static_cast<int>(gridDim.x) - a.Hq, sh);
+        fin_mean_tokens<MT>(a, b - a.Hq, static_cast<int>(gridDim.x) - a.Hq, sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -882,7 +890,7 @@ __global__ void __launch_bounds__(256) attn_finalize_batched_kernel(const FinBat
     const int m = blk - merges;
     const int i = batch_find(b.mean_base, b.nseq, m);
     const FinArgs a = fin_batch_args(b, i);
-    fin_mean_tokens(a, m - b.mean_base[i], b.mean_base[i + 1] - b.mean_base[i], sh);
+    fin_mean_tokens<kMeanTokens>(a, m - b.mean_base[i], b.mean_base[i + 1] - b.mean_base[i], sh);
 }
 
 template <int CPL, int GP>
@@ -1146,14 +1154,18 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
     f.head_w = head_w;
     f.head_w_ld = head_w_ld;
     f.fb = fb ? *fb : Feedback{};
+    const int mt = plan.token_ub >= kMeanLongFrom ? kMeanTokensLong : kMeanTokens;
     int mean_wgs = 0;
     if (weights) {
-        const int blocks = (std::max(plan.token_ub, 1) + kMeanTokens - 1) / kMeanTokens;
+        const int blocks = (std::max(plan.token_ub, 1) + mt - 1) / mt;
         const int per_wg = (blocks + kMeanMaxWgs - 1) / kMeanMaxWgs;
         mean_wgs = (blocks + per_wg - 1) / per_wg;
     }
     const size_t lds = sizeof(float) * std::max<size_t>(8 + 4 * 256, 2 * static_cast<size_t>(in.Hq) + 256 * 4);
-    hipLaunchKernelGGL(attn_finalize_kernel, dim3(in.Hq + mean_wgs), dim3(256), lds, stream, f);
+    if (mt == kMeanTokensLong)
+        hipLaunchKernelGGL(attn_finalize_kernel<kMeanTokensLong>, dim3(in.Hq + mean_wgs), dim3(256), lds, stream, f);
+    else
+        hipLaunchKernelGGL(attn_finalize_kernel<kMeanTokens>, dim3(in.Hq + mean_wgs), dim3(256), lds, stream, f);
     TT_LAUNCH_CHECK();
     return TT_OK;
 }
