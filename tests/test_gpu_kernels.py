@@ -323,6 +323,8 @@ def _tiered_layer(C, Hq, Hkv, D, ctx, fp16, seed, k_outliers=False, student_t=Fa
     ("mha-8k", 32, 32, 8192, False),
     ("llama3-8b-32k", 32, 8, 32768, False),
     ("llama3-8b-32k-fp16", 32, 8, 32768, True),
+    # 7:1 GQA (8-head groups) and 128-token mean-weight blocks (over 64k tokens)
+    ("qwen2-7b-128k", 28, 4, 131072, False),
 ])
 def test_full_size_layer_vs_oracle(C, oracle, name, Hq, Hkv, ctx, fp16):
     D = 128
