@@ -312,10 +312,10 @@ __device__ __forceinline__ void split_body(const SplitArgs& a, const int split, 
             tm = fmaxf(tm, shfl_xor(tm, 16));
             tm = fmaxf(tm, shfl_xor(tm, 32));
             const float mn = fmaxf(m[g], tm);
-            const float alpha = (m[g] == kNegInf) ? 0.0f : exp2f(m[g] - mn);
+            const float alpha = (m[g] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(m[g] - mn);
             float p[4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) p[i] = (s[i][g] == kNegInf) ? 0.0f : exp2f(s[i][g] - mn);
+            for (int i = 0; i < 4; ++i) p[i] = (s[i][g] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(s[i][g] - mn);
             l[g] = __builtin_fmaf(l[g], alpha, (p[0] + p[1]) + (p[2] + p[3]));
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
@@ -368,7 +368,7 @@ __device__ __forceinline__ void split_body(const SplitArgs& a, const int split, 
 #pragma unroll
             for (int w = 0; w < 4; ++w) {
                 const float mw = sm_m[w * GP + g];
-                const float f = (mw == kNegInf) ? 0.0f : exp2f(mw - M);
+                const float f = (mw == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(mw - M);
                 A = __builtin_fmaf(f, sm_acc[(w * GP + g) * D + c], A);
                 L = __builtin_fmaf(f, sm_l[w * GP + g], L);
             }
@@ -508,14 +508,14 @@ __device__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
         __syncthreads();
         const float Mb = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
         const float Mn = fmaxf(M, Mb);
-        const float ws = wave_sum(mt == kNegInf ? 0.0f : exp2f(mt - Mn) * lt);
+        const float ws = wave_sum(mt == kNegInf ? 0.0f : __builtin_amdgcn_exp2f(mt - Mn) * lt);
         __syncthreads();
         if (lane == 0) sh[4 + wave] = ws;
-        const float al = (M == kNegInf) ? 0.0f : exp2f(M - Mn);
+        const float al = (M == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(M - Mn);
         A.x *= al; A.y *= al; A.z *= al; A.w *= al;
 #pragma unroll
         for (int u = 0; u < kMergeU; ++u) {
-            const float f = (mv[u] == kNegInf) ? 0.0f : exp2f(mv[u] - Mn);
+            const float f = (mv[u] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(mv[u] - Mn);
             A.x = __builtin_fmaf(f, v[u].x, A.x);
             A.y = __builtin_fmaf(f, v[u].y, A.y);
             A.z = __builtin_fmaf(f, v[u].z, A.z);
@@ -524,7 +524,7 @@ __device__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
         // splits beyond kMergeU per group in this block of 256 (groups < 16 only)
         for (int j = j0 + g + kMergeU * groups; g < groups && j < a.nsplit && j < j0 + 256; j += groups) {
             const float mj = ml[2 * j];
-            const float f = (mj == kNegInf) ? 0.0f : exp2f(mj - Mn);
+            const float f = (mj == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(mj - Mn);
             const float4 w = *reinterpret_cast<const float4*>(base + static_cast<size_t>(j) * a.D);
             A.x = __builtin_fmaf(f, w.x, A.x);
             A.y = __builtin_fmaf(f, w.y, A.y);

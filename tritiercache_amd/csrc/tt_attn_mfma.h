@@ -433,7 +433,7 @@ __device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit,
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             const float* dg = dl + (w * GP + g) * (2 + kMfD);
-            const float f = (dg[0] == kNegInf) ? 0.0f : exp2f(dg[0] - M);  // waves without tiles add nothing
+            const float f = (dg[0] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(dg[0] - M);  // waves without tiles add nothing
             A = __builtin_fmaf(f, dg[2 + c], A);
             Ls = __builtin_fmaf(f, dg[1], Ls);
         }
@@ -855,7 +855,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             // a wave without pairs has m = -1e30, l = 0, acc = 0: it adds nothing
-            const float f = exp2f(sm_m[w * GP + g] - M);
+            const float f = __builtin_amdgcn_exp2f(sm_m[w * GP + g] - M);
             A = __builtin_fmaf(f, sm_acc[(w * GP + g) * kMfD + c] + sm_z[w * GP + g], A);
             Ls = __builtin_fmaf(f, sm_l[w * GP + g], Ls);
         }
