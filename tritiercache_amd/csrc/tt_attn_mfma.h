@@ -75,7 +75,15 @@ struct MfLds {
     static_assert(MERGE <= 4 * BYTES, "merge area must fit in the staging area");
     // the workgroup's query heads [GP][128] f32, after the four staging areas
     static constexpr int QL = 4 * BYTES;
-    static constexpr int TOTAL = QL + GP * kMfD * 4;
+    // 128 zero f16 coefficients (a B row that contributes nothing)
+    static constexpr int ZERO = QL + GP * kMfD * 4;
+    // Per-wave logits of the last LB_PAIRS pairs, [GP][LB_PAIRS * 32] f32: they
+    // reach memory in runs of LB_PAIRS * 128 bytes per head. Eight heads store
+    // their logits directly (buffering them measured slower there).
+    static constexpr int LB_PAIRS = GP > 4 ? 0 : 4;
+    static constexpr int LB = ZERO + 256;
+    static constexpr int LB_WAVE = GP * LB_PAIRS * 32 * 4;
+    static constexpr int TOTAL = LB + 4 * LB_WAVE;
 };
 
 // LDS of an FP32-tier workgroup (byte offsets): the query heads, then the
@@ -87,18 +95,37 @@ struct DnLds {
     static constexpr int TOTAL = PART + 4 * GP * (2 + kMfD) * 4;
 };
 
+// max(a, b) for operands that are never NaN: one v_max_f32, without the
+// quieting of the operands that fmaxf adds for values it cannot see the origin of.
+__device__ __forceinline__ float fmax_nn(float a, float b) {
+    float r;
+    asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+// max(|a|, |b|), likewise
+__device__ __forceinline__ float fmax_abs_nn(float a, float b) {
+    float r;
+    asm("v_max_f32_e64 %0, |%1|, |%2|" : "=v"(r) : "v"(a), "v"(b));
+    return r;
+}
+
 // Reductions over the four 16-lane rows of a wave (lanes n, n+16, n+32, n+48).
 __device__ __forceinline__ float xrow_max(float x) {
     const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    x = fmaxf(__uint_as_float(s[0]), __uint_as_float(s[1]));
+    x = fmax_nn(__uint_as_float(s[0]), __uint_as_float(s[1]));
     const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+    return fmax_nn(__uint_as_float(t[0]), __uint_as_float(t[1]));
 }
 __device__ __forceinline__ float xrow_sum(float x) {
     const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     x = __uint_as_float(s[0]) + __uint_as_float(s[1]);
     const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(t[0]) + __uint_as_float(t[1]);
+}
+// x[l] + x[l ^ 16]
+__device__ __forceinline__ float xrow_pair_sum(float x) {
+    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
 }
 // x[l] + x[l ^ 32]
 __device__ __forceinline__ float xhalf_sum(float x) {
@@ -456,6 +483,14 @@ __device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit,
 // logits and run the same softmax. The PV operand likewise puts p vs high in
 // row h and low in row h + 8; the two accumulator rows are added once at the
 // end. Columns / rows of padding heads repeat head 0 and are never stored.
+//
+// Four heads fill only half of those columns, so there the two tiles of a
+// pair share one score block instead (TP): tile T sits in columns 4T + h
+// (high) and 8 + 4T + h (low). Its four QK MFMAs read a zero coefficient row
+// in the other tile's columns, so one accumulator chain over both tiles
+// leaves every column the logits of its own tile, and each lane runs the
+// softmax over 4 tokens rather than 8. In the PV operand the K elements
+// of the other tile are zero, which keeps the token order of the V codes.
 template <int GP, typename MetaT>
 __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split, const int kvh, const int chunk,
                                             char* lds) {
@@ -473,6 +508,10 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     const int hn = n & 7;      // query head of column n
     const bool lo_col = n >= 8;
     const float negm_col = lo_col ? -1.0f : 0.0f;  // PV operand: lo rows take the remainder
+    constexpr bool TP = GP == 4;
+    constexpr int NT = TP ? 1 : 2;                 // tiles held by one lane's scores
+    const int ctile = TP ? (n >> 2) & 1 : 0;       // TP: the tile of column n
+    const int chead = TP ? n & 3 : hn;             // query head of column n
     const int Hkv = in.Hkv;
 
     int n0 = in.n0, n1 = in.n1, n2 = in.n2, nb = in.num_blocks;
@@ -574,6 +613,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     const int wp0 = pb + part_begin(pe - pb, wave, 4);
     const int wp1 = pb + part_begin(pe - pb, wave + 1, 4);
     if (wp0 < wp1) fetch(wp0);
+    if (TP && threadIdx.x < 64) reinterpret_cast<uint32_t*>(lds + L::ZERO)[threadIdx.x] = 0u;
     __syncthreads();
 
     // Q' = Q 2^-e per head (e = exponent of max |Q_h|) in the coefficient
@@ -603,18 +643,19 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         for (int j = 0; j < 8; ++j) qv[pp][j] = __builtin_amdgcn_ldexpf(qv[pp][j], -e);
         cpass[pp] = (h < gc) ? __builtin_amdgcn_ldexpf(a.scale2, e) : 0.0f;
     }
-    // Column scale of query head hn: lane 16 (hn & 3) of pass hn >> 2 holds it.
+    // Column scale of query head chead: lane 16 (chead & 3) of pass chead >> 2 holds it.
     float ccol = 0.0f;
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
-        const float t = __shfl(cpass[pp], 16 * (hn & 3), 64);
-        if ((hn >> 2) == pp) ccol = t;
+        const float t = __shfl(cpass[pp], 16 * (chead & 3), 64);
+        if ((chead >> 2) == pp) ccol = t;
     }
     float crow[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) crow[r] = __builtin_amdgcn_ldexpf(ccol, -2 * r);
-    const int bhead = hn < GP ? hn : 0;
+    const int bhead = chead < GP ? chead : 0;
     const int brow = bhead + (lo_col ? GP : 0);
+    const char* zero_l = lds + L::ZERO;
 
     const uint32_t kmask = (3u << (2 * (lane & 3))) | (3u << (16 + 2 * (lane & 3)));
     uint32_t one024;
@@ -691,6 +732,9 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         }
     };
 
+    constexpr int kLbTok = L::LB_PAIRS * 32;  // floats per head in the logits buffer (none: direct stores)
+    float* lb = reinterpret_cast<float*>(lds + L::LB + wave * L::LB_WAVE);
+    int pbuf = wp0;  // first pair held in the logits buffer
     for (int p = wp0; p < wp1; ++p) {
         const uint32_t vmask = stage();
         if (p + 1 < wp1) fetch(p + 1);
@@ -699,71 +743,142 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         if (W == 1 && L::NBT == 2) coeffs(1, 1);
         wave_lds_sync();
 
-        float s2[2][4];
+        // s2[i][r]: logit of token 4 gk + r of tile tt(i) in column n, tt(i) = ctile
+        // with the tiles packed (TP), else i.
+        float s2[NT][4];
+        auto tt = [&](const int i) { return TP ? ctile : i; };
+        if constexpr (TP) {
+            // a chain per tile; the other tile's columns read the zero row
+            mf_f4 dt[2];
 #pragma unroll
-        for (int tile = 0; tile < 2; ++tile) {
-            const int tb = (W == 2 || L::NBT == 1) ? 0 : tile;
-            if (W == 1 && L::NBT == 1 && tile == 1) {
-                wave_lds_sync();  // tile 0's coefficients and bias are read
-                coeffs(1, 0);
-                wave_lds_sync();
+            for (int tile = 0; tile < 2; ++tile) {
+                mf_f4& d = dt[tile];
+                d = mf_f4{0.0f, 0.0f, 0.0f, 0.0f};
+                const int tb = (W == 2) ? 0 : tile;
+                const mf_u4* ka = reinterpret_cast<const mf_u4*>(kt_l + (tile * 4 + ((lane & 15) >> 2)) * kKTS + 8 * gk);
+                const mf_u4 ra = ka[0], rb = ka[1];
+                const char* kbase =
+                    (tile == ctile) ? bhl_l + tb * L::BHL_TILE + (brow * kBRS + 32 * gk) * 2 : zero_l + 64 * gk;
+                const mf_u4* kb = reinterpret_cast<const mf_u4*>(kbase);
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const uint32_t x = (s < 2) ? ra[2 * s] : rb[2 * s - 4];
+                    const uint32_t y = (s < 2) ? ra[2 * s + 1] : rb[2 * s - 3];
+                    const mf_u4 av = {code_f16(x, kmask, one024), code_f16(x >> 8, kmask, one024),
+                                      code_f16(y, kmask, one024), code_f16(y >> 8, kmask, one024)};
+                    d = mfma16x16x32(av, kb[s], d);
+                }
             }
-            // A: codes of token t = lane & 15 (k = t & 3), channels 32 gk .. 32 gk + 31.
-            const mf_u4* ka = reinterpret_cast<const mf_u4*>(kt_l + (tile * 4 + ((lane & 15) >> 2)) * kKTS + 8 * gk);
-            const mf_u4 ra = ka[0], rb = ka[1];
-            const mf_u4* kb = reinterpret_cast<const mf_u4*>(bhl_l + tb * L::BHL_TILE + (brow * kBRS + 32 * gk) * 2);
-            mf_f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+            const float bc = bias_l[((W == 2) ? 0 : ctile) * 8 + bhead] * ccol;
+            const mf_f4 d = dt[0] + dt[1];
 #pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const uint32_t x = (s < 2) ? ra[2 * s] : rb[2 * s - 4];
-                const uint32_t y = (s < 2) ? ra[2 * s + 1] : rb[2 * s - 3];
-                const mf_u4 av = {code_f16(x, kmask, one024), code_f16(x >> 8, kmask, one024),
-                                  code_f16(y, kmask, one024), code_f16(y >> 8, kmask, one024)};
-                d = mfma16x16x32(av, kb[s], d);
+            for (int r = 0; r < 4; ++r) s2[0][r] = __builtin_fmaf(d[r] + dpp<0x128>(d[r]), crow[r], bc);
+        } else {
+#pragma unroll
+            for (int tile = 0; tile < 2; ++tile) {
+                const int tb = (W == 2 || L::NBT == 1) ? 0 : tile;
+                if (W == 1 && L::NBT == 1 && tile == 1) {
+                    wave_lds_sync();  // tile 0's coefficients and bias are read
+                    coeffs(1, 0);
+                    wave_lds_sync();
+                }
+                // A: codes of token t = lane & 15 (k = t & 3), channels 32 gk .. 32 gk + 31.
+                const mf_u4* ka = reinterpret_cast<const mf_u4*>(kt_l + (tile * 4 + ((lane & 15) >> 2)) * kKTS + 8 * gk);
+                const mf_u4 ra = ka[0], rb = ka[1];
+                const mf_u4* kb = reinterpret_cast<const mf_u4*>(bhl_l + tb * L::BHL_TILE + (brow * kBRS + 32 * gk) * 2);
+                mf_f4 d = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                    const uint32_t x = (s < 2) ? ra[2 * s] : rb[2 * s - 4];
+                    const uint32_t y = (s < 2) ? ra[2 * s + 1] : rb[2 * s - 3];
+                    const mf_u4 av = {code_f16(x, kmask, one024), code_f16(x >> 8, kmask, one024),
+                                      code_f16(y, kmask, one024), code_f16(y >> 8, kmask, one024)};
+                    d = mfma16x16x32(av, kb[s], d);
+                }
+                const float bc = bias_l[tb * 8 + bhead] * ccol;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) s2[tile][r] = __builtin_fmaf(d[r] + dpp<0x128>(d[r]), crow[r], bc);
             }
-            const float bc = bias_l[tb * 8 + bhead] * ccol;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) s2[tile][r] = __builtin_fmaf(d[r] + dpp<0x128>(d[r]), crow[r], bc);
         }
 
         const bool full = (vmask == 0xffffffffu);
         if (!full) {
 #pragma unroll
-            for (int tile = 0; tile < 2; ++tile)
+            for (int i = 0; i < NT; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    if (!((vmask >> (16 * tile + 4 * gk + r)) & 1u)) s2[tile][r] = kNegInf;
+                    if (!((vmask >> (16 * tt(i) + 4 * gk + r)) & 1u)) s2[i][r] = kNegInf;
         }
-        if (a.logits && n < gc) {
-            float* row = a.logits + static_cast<size_t>(kvh * G + g0 + n) * a.ld + Nd + 32 * p + 4 * gk;
+        // The columns of the high parts leave the logits of their head in the
+        // wave's buffer; after LB_PAIRS pairs (or the last) it goes to memory.
+        if (L::LB_PAIRS == 0 && a.logits && !lo_col && chead < gc) {
+            float* row = a.logits + static_cast<size_t>(kvh * G + g0 + chead) * a.ld + Nd + 32 * p + 4 * gk;
             if (32 * p + 32 <= nslots) {
 #pragma unroll
-                for (int tile = 0; tile < 2; ++tile)
+                for (int i = 0; i < NT; ++i)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) row[16 * tile + r] = s2[tile][r];
+                    for (int r = 0; r < 4; ++r) row[16 * tt(i) + r] = s2[i][r];
             } else {
 #pragma unroll
-                for (int tile = 0; tile < 2; ++tile)
+                for (int i = 0; i < NT; ++i)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        if (32 * p + 16 * tile + 4 * gk + r < nslots) row[16 * tile + r] = s2[tile][r];
+                        if (32 * p + 16 * tt(i) + 4 * gk + r < nslots) row[16 * tt(i) + r] = s2[i][r];
+            }
+        }
+        if (L::LB_PAIRS > 0 && a.logits) {
+            if (!lo_col && chead < GP) {
+#pragma unroll
+                for (int i = 0; i < NT; ++i)
+                    *reinterpret_cast<float4*>(lb + chead * kLbTok + 32 * (p - pbuf) + 16 * tt(i) + 4 * gk) =
+                        make_float4(s2[i][0], s2[i][1], s2[i][2], s2[i][3]);
+            }
+            if (p - pbuf == L::LB_PAIRS - 1 || p == wp1 - 1) {
+                wave_lds_sync();
+                // lane: token quad `lane` of the buffered pairs, every head of the group
+                if (lane < (p + 1 - pbuf) * 8) {
+                    const int tok = 32 * pbuf + 4 * lane;
+                    for (int hh = 0; hh < gc; ++hh) {
+                        const float4 v = *reinterpret_cast<const float4*>(lb + hh * kLbTok + 4 * lane);
+                        float* dst = a.logits + static_cast<size_t>(kvh * G + g0 + hh) * a.ld + Nd + tok;
+                        if (tok + 4 <= nslots) {
+                            *reinterpret_cast<float4*>(dst) = v;
+                        } else {
+                            if (tok < nslots) dst[0] = v.x;
+                            if (tok + 1 < nslots) dst[1] = v.y;
+                            if (tok + 2 < nslots) dst[2] = v.z;
+                        }
+                    }
+                }
+                wave_lds_sync();
+                pbuf = p + 1;
             }
         }
 
-        // V scale / zero of this lane's tokens: [tile 0 r 0..3, tile 1 r 0..3].
-        const float4 va = *reinterpret_cast<const float4*>(vs_l + 8 * gk);
-        const float4 vb = *reinterpret_cast<const float4*>(vs_l + 8 * gk + 4);
-        const float4 za = *reinterpret_cast<const float4*>(vz_l + 8 * gk);
-        const float4 zb = *reinterpret_cast<const float4*>(vz_l + 8 * gk + 4);
-        const float vsv[2][4] = {{va.x, va.y, va.z, va.w}, {vb.x, vb.y, vb.z, vb.w}};
-        const float vzv[2][4] = {{za.x, za.y, za.z, za.w}, {zb.x, zb.y, zb.z, zb.w}};
+        // V scale / zero of this lane's tokens ([tile 0 r 0..3, tile 1 r 0..3] at 8 gk).
+        float vsv[NT][4], vzv[NT][4];
+#pragma unroll
+        for (int i = 0; i < NT; ++i) {
+            const float4 vq = *reinterpret_cast<const float4*>(vs_l + 8 * gk + 4 * tt(i));
+            const float4 zq = *reinterpret_cast<const float4*>(vz_l + 8 * gk + 4 * tt(i));
+            vsv[i][0] = vq.x; vsv[i][1] = vq.y; vsv[i][2] = vq.z; vsv[i][3] = vq.w;
+            vzv[i][0] = zq.x; vzv[i][1] = zq.y; vzv[i][2] = zq.z; vzv[i][3] = zq.w;
+        }
 
-        float mx = fmaxf(fmaxf(fmaxf(s2[0][0], s2[0][1]), fmaxf(s2[0][2], s2[0][3])),
-                         fmaxf(fmaxf(s2[1][0], s2[1][1]), fmaxf(s2[1][2], s2[1][3])));
-        float vmx = fmaxf(fmaxf(fmaxf(fabsf(va.x), fabsf(va.y)), fmaxf(fabsf(va.z), fabsf(va.w))),
-                          fmaxf(fmaxf(fabsf(vb.x), fabsf(vb.y)), fmaxf(fabsf(vb.z), fabsf(vb.w))));
+        float mx = fmax_nn(fmax_nn(s2[0][0], s2[0][1]), fmax_nn(s2[0][2], s2[0][3]));
+        float vmx = fmax_nn(fmax_abs_nn(vsv[0][0], vsv[0][1]), fmax_abs_nn(vsv[0][2], vsv[0][3]));
+#pragma unroll
+        for (int i = 1; i < NT; ++i) {
+            mx = fmax_nn(mx, fmax_nn(fmax_nn(s2[i][0], s2[i][1]), fmax_nn(s2[i][2], s2[i][3])));
+            vmx = fmax_nn(vmx, fmax_nn(fmax_abs_nn(vsv[i][0], vsv[i][1]), fmax_abs_nn(vsv[i][2], vsv[i][3])));
+        }
         mx = xrow_max(mx);
         vmx = xrow_max(vmx);
+        if constexpr (TP) {
+            // column n +- 4 holds the same head's other tile
+            mx = fmax_nn(mx, dpp<0x124>(mx));
+            vmx = fmax_nn(vmx, dpp<0x124>(vmx));
+        }
         const int ev = (vmx > 0.0f) ? __builtin_amdgcn_frexp_expf(vmx) : 0;
         const float cand = mx - static_cast<float>(13 - ev);
         const bool up = cand > m_run + kMfTau;
@@ -781,20 +896,29 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
             m_run = mn;
         }
 
-        float pv[2][4];
+        float pv[NT][4];
         float lsum = 0.0f;
 #pragma unroll
-        for (int tile = 0; tile < 2; ++tile)
+        for (int i = 0; i < NT; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float e = __builtin_amdgcn_exp2f(s2[tile][r] - m_run);  // flushes below 2^-126
+                const float e = __builtin_amdgcn_exp2f(s2[i][r] - m_run);  // flushes below 2^-126
                 lsum += e;
-                pz = __builtin_fmaf(e, vzv[tile][r], pz);
-                pv[tile][r] = e * vsv[tile][r];
+                pz = __builtin_fmaf(e, vzv[i][r], pz);
+                pv[i][r] = e * vsv[i][r];
             }
         l_run += lsum;
-        const mf_u4 ap = {split_half(pv[0][0], pv[0][2], negm_col), split_half(pv[0][1], pv[0][3], negm_col),
-                          split_half(pv[1][0], pv[1][2], negm_col), split_half(pv[1][1], pv[1][3], negm_col)};
+        mf_u4 ap;
+        if constexpr (TP) {
+            // K elements 0..3 are tile 0's tokens, 4..7 tile 1's (the V code order)
+            const uint32_t h0 = split_half(pv[0][0], pv[0][2], negm_col);
+            const uint32_t h1 = split_half(pv[0][1], pv[0][3], negm_col);
+            ap = ctile ? mf_u4{0u, 0u, h0, h1} : mf_u4{h0, h1, 0u, 0u};
+        } else {
+            ap = mf_u4{split_half(pv[0][0], pv[0][2], negm_col), split_half(pv[0][1], pv[0][3], negm_col),
+                       split_half(pv[NT - 1][0], pv[NT - 1][2], negm_col),
+                       split_half(pv[NT - 1][1], pv[NT - 1][3], negm_col)};
+        }
 
         // B: codes of channel 4 beta + k for the lane's 8 tokens,
         // beta = n (nsteps 0..3) and n + 16 (nsteps 4..7), k = nstep & 3.
@@ -817,11 +941,23 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
 
     l_run = xrow_sum(l_run);
     pz = xrow_sum(pz);
+    if constexpr (TP) {
+        // add the other tile's column of the head
+        l_run += dpp<0x124>(l_run);
+        pz += dpp<0x124>(pz);
+    }
     // rows h + 8 (low parts, lanes 32..63) onto rows h (lanes 0..31)
 #pragma unroll
     for (int s = 0; s < 8; ++s)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[s][r] = xhalf_sum(acc[s][r]);
+    if constexpr (TP) {
+        // rows 4 + h (tile 1, lanes 16..31) onto rows h (lanes 0..15)
+#pragma unroll
+        for (int s = 0; s < 8; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[s][r] = xrow_pair_sum(acc[s][r]);
+    }
 
     __syncthreads();  // every wave is done with its staging area
     float* sm_m = reinterpret_cast<float*>(lds);  // [4][GP]
