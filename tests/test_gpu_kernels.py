@@ -325,6 +325,10 @@ def _tiered_layer(C, Hq, Hkv, D, ctx, fp16, seed, k_outliers=False, student_t=Fa
     ("llama3-8b-32k-fp16", 32, 8, 32768, True),
     # 7:1 GQA (8-head groups) and 128-token mean-weight blocks (over 64k tokens)
     ("qwen2-7b-128k", 28, 4, 131072, False),
+    # long enough that every wave of the four-head and one-head groups takes
+    # more pairs than its logits buffer holds (flushes inside the loop)
+    ("llama3-8b-96k", 32, 8, 98304, False),
+    ("mha-32k", 32, 32, 32768, True),
 ])
 def test_full_size_layer_vs_oracle(C, oracle, name, Hq, Hkv, ctx, fp16):
     D = 128
