@@ -62,6 +62,7 @@ struct AttnPlan {
     int nsplit_d = 1;    // VALU workgroups
     int ld = 0;          // logits row stride (floats)
     int token_ub = 0;    // upper bound on attended tokens
+    int dense_delay = 0; // wait of the FP32-tier workgroups before their first load (10 ns ticks)
     size_t off_ml = 0, off_acc = 0, off_rowstat = 0, off_logits = 0, bytes = 0;
     bool logits = false;
 };

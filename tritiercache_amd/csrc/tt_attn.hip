@@ -123,6 +123,7 @@ struct SplitArgs {
     int nsplit_p;    // matrix-core workgroups over the packed store: slots [0, nsplit_p)
     int nsplit_d;    // VALU workgroups: slots [nsplit_p, nsplit)
     int wd, wp;      // tile cost weights: dense, packed
+    int dense_delay; // FP32-tier workgroups wait this many 10 ns ticks before their first tile load
 };
 
 // LDS of the VALU tile loop: per-wave (max, sum, acc[D]) for the final merge.
@@ -833,6 +834,7 @@ attn_batched_kernel(const BatchArgs b) {
     a.nsplit_d = a.nsplit - a.nsplit_p;
     a.wd = 8;
     a.wp = 1;
+    a.dense_delay = 0;
     const int kvh = hz / b.chunks, chunk = hz - kvh * b.chunks;
     if (s >= a.nsplit_p) {
         dense_body<GP>(a, s - a.nsplit_p, kvh, chunk, lds);
@@ -1076,6 +1078,20 @@ AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs,
             p.nsplit_d = static_cast<int>(nd);
             p.nsplit_p = static_cast<int>(std::max<long long>(1, wgs - nd));
         }
+        // The FP32 workgroups' first tiles, requested at the start, compete
+        // with the packed waves' first pairs. When a packed wave has at least
+        // three times the work items of an FP32 wave, the FP32 workgroups wait
+        // about twice the time the first pairs take to arrive at 5 TB/s (at
+        // most 4 us) before their first tile load; they still finish within
+        // the packed waves' time.
+        const long long tp = (pairs + 4LL * p.nsplit_p - 1) / (4LL * p.nsplit_p);
+        const long long td = p.nsplit_d > 0 ? (dense_tiles + 4LL * p.nsplit_d - 1) / (4LL * p.nsplit_d) : 0;
+        if (td > 0 && tp >= 3 * td) {
+            const long long m = meta_fp16 ? 2 : 4;
+            const long long pair_bytes = 2 * (512 + 256 * m / W + 512 + 32 * m + 128);
+            const long long burst = std::min(pairs, 4LL * p.nsplit_p) * heads * pair_bytes;
+            p.dense_delay = static_cast<int>(std::min<long long>(400, burst / 25000));
+        }
     } else {
         // One round of resident workgroups, but at least ~32 packed-tile
         // units of work per workgroup so the merge traffic stays small.
@@ -1115,6 +1131,7 @@ int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipS
     a.nsplit_d = plan.nsplit_d;
     a.wd = 8;
     a.wp = 1;
+    a.dense_delay = plan.dense_delay;
     const int G = in.Hq / in.Hkv;
     const int gp = gp_for(G);
     const int chunks = (G + gp - 1) / gp;

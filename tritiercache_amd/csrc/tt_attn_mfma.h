@@ -446,6 +446,12 @@ __device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit,
     float* dl = reinterpret_cast<float*>(lds + L::PART);
     load_q_lds<GP>(in, kvh, g0, gc, q_l);
     DenseTile dt;
+    if (a.dense_delay > 0) {
+        // bounded by the constant-rate real-time counter
+        const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+        while (__builtin_amdgcn_s_memrealtime() - t0 < static_cast<unsigned long long>(a.dense_delay))
+            __builtin_amdgcn_s_sleep(8);
+    }
     if (d0 + wave < d1) dense_load(in, dv, kvh, d0 + wave, dt);
     __syncthreads();
     dense_share<GP>(a, dv, d0, d1, kvh, g0, gc, wave, q_l, dt, dl);
