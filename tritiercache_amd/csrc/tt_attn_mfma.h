@@ -753,18 +753,25 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         // with the tiles packed (TP), else i.
         float s2[NT][4];
         auto tt = [&](const int i) { return TP ? ctile : i; };
-        // V scale / zero of this lane's tokens ([tile 0 r 0..3, tile 1 r 0..3] at 8 gk).
+        // V scale / zero of this lane's tokens ([tile 0 r 0..3, tile 1 r 0..3] at 8 gk)
+        // and the pair's V codes. Four-head groups read them ahead of the QK
+        // MFMAs (off the chain that follows them); eight-head groups after the
+        // scores, as read ahead they would not fit in 168 VGPRs.
         float vsv[NT][4], vzv[NT][4];
+        uint2 q0, q1;
+        auto read_v = [&]() {
 #pragma unroll
-        for (int i = 0; i < NT; ++i) {
-            const float4 vq = *reinterpret_cast<const float4*>(vs_l + 8 * gk + 4 * tt(i));
-            const float4 zq = *reinterpret_cast<const float4*>(vz_l + 8 * gk + 4 * tt(i));
-            vsv[i][0] = vq.x; vsv[i][1] = vq.y; vsv[i][2] = vq.z; vsv[i][3] = vq.w;
-            vzv[i][0] = zq.x; vzv[i][1] = zq.y; vzv[i][2] = zq.z; vzv[i][3] = zq.w;
-        }
-        const uint2* vtr = reinterpret_cast<const uint2*>(vt_l);
-        const uint2 q0 = vtr[n * (kVTS / 2) + gk];
-        const uint2 q1 = vtr[(n + 16) * (kVTS / 2) + gk];
+            for (int i = 0; i < NT; ++i) {
+                const float4 vq = *reinterpret_cast<const float4*>(vs_l + 8 * gk + 4 * tt(i));
+                const float4 zq = *reinterpret_cast<const float4*>(vz_l + 8 * gk + 4 * tt(i));
+                vsv[i][0] = vq.x; vsv[i][1] = vq.y; vsv[i][2] = vq.z; vsv[i][3] = vq.w;
+                vzv[i][0] = zq.x; vzv[i][1] = zq.y; vzv[i][2] = zq.z; vzv[i][3] = zq.w;
+            }
+            const uint2* vtr = reinterpret_cast<const uint2*>(vt_l);
+            q0 = vtr[n * (kVTS / 2) + gk];
+            q1 = vtr[(n + 16) * (kVTS / 2) + gk];
+        };
+        if constexpr (TP) read_v();
         if constexpr (TP) {
             // a chain per tile; the other tile's columns read the zero row
             mf_f4 dt[2];
@@ -874,6 +881,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         }
 
 
+        if constexpr (!TP) read_v();
         float mx = fmax_nn(fmax_nn(s2[0][0], s2[0][1]), fmax_nn(s2[0][2], s2[0][3]));
         float vmx = fmax_nn(fmax_abs_nn(vsv[0][0], vsv[0][1]), fmax_abs_nn(vsv[0][2], vsv[0][3]));
 #pragma unroll
