@@ -669,21 +669,29 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
         const int h = h0 + (t >> 3), j0 = t & 7;
         const float* ml = a.part_ml + static_cast<size_t>(h < Hq ? h : 0) * a.nsplit * 2;
         float mx = kNegInf, ls = 0.0f;
-        for (int jb = j0; jb < a.nsplit; jb += 8 * kMergeU) {
-            float2 v[kMergeU];  // (m, l) of split jb + 8 u
+        constexpr int kU4 = 8;
+        for (int jb = 2 * j0; jb < a.nsplit; jb += 16 * kU4) {
+            float2 v[2 * kU4];  // (m, l) of splits jb + 16 u and jb + 16 u + 1
 #pragma unroll
-            for (int u = 0; u < kMergeU; ++u) {
-                const int j = jb + 8 * u;
-                v[u] = j < a.nsplit ? *reinterpret_cast<const float2*>(ml + 2 * j) : make_float2(kNegInf, 0.0f);
+            for (int u = 0; u < kU4; ++u) {
+                const int j = jb + 16 * u;
+                if (j + 1 < a.nsplit) {
+                    const float4 w = *reinterpret_cast<const float4*>(ml + 2 * j);
+                    v[2 * u] = make_float2(w.x, w.y);
+                    v[2 * u + 1] = make_float2(w.z, w.w);
+                } else {
+                    v[2 * u] = j < a.nsplit ? *reinterpret_cast<const float2*>(ml + 2 * j) : make_float2(kNegInf, 0.0f);
+                    v[2 * u + 1] = make_float2(kNegInf, 0.0f);
+                }
             }
             float bm = kNegInf;
 #pragma unroll
-            for (int u = 0; u < kMergeU; ++u) bm = fmaxf(bm, v[u].x);
+            for (int u = 0; u < 2 * kU4; ++u) bm = fmaxf(bm, v[u].x);
             const float mn = fmaxf(mx, bm);
             float bs = 0.0f;
             // hardware exp2: arguments <= 0, results below 2^-126 flush to 0
 #pragma unroll
-            for (int u = 0; u < kMergeU; ++u)
+            for (int u = 0; u < 2 * kU4; ++u)
                 bs += (v[u].x == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(v[u].x - mn) * v[u].y;
             ls = ((mx == kNegInf) ? 0.0f : ls * __builtin_amdgcn_exp2f(mx - mn)) + bs;
             mx = mn;
