@@ -889,17 +889,20 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
             mx = fmax_nn(mx, fmax_nn(fmax_nn(s2[i][0], s2[i][1]), fmax_nn(s2[i][2], s2[i][3])));
             vmx = fmax_nn(vmx, fmax_nn(fmax_abs_nn(vsv[i][0], vsv[i][1]), fmax_abs_nn(vsv[i][2], vsv[i][3])));
         }
-        mx = xrow_max(mx);
-        vmx = xrow_max(vmx);
-        if constexpr (TP) {
-            // column n +- 4 holds the same head's other tile
-            mx = fmax_nn(mx, dpp<0x124>(mx));
-            vmx = fmax_nn(vmx, dpp<0x124>(vmx));
-        }
-        const int ev = (vmx > 0.0f) ? __builtin_amdgcn_frexp_expf(vmx) : 0;
-        const float cand = mx - static_cast<float>(13 - ev);
-        const bool up = cand > m_run + kMfTau;
-        if (__ballot(up)) {
+        // Each lane tests the bound on its own tokens; the reductions over the
+        // head's lanes (and the rescale) run only when some lane breaks it.
+        const int evl = (vmx > 0.0f) ? __builtin_amdgcn_frexp_expf(vmx) : 0;
+        if (__ballot(mx - static_cast<float>(13 - evl) > m_run + kMfTau)) {
+            mx = xrow_max(mx);
+            vmx = xrow_max(vmx);
+            if constexpr (TP) {
+                // column n +- 4 holds the same head's other tile
+                mx = fmax_nn(mx, dpp<0x124>(mx));
+                vmx = fmax_nn(vmx, dpp<0x124>(vmx));
+            }
+            const int ev = (vmx > 0.0f) ? __builtin_amdgcn_frexp_expf(vmx) : 0;
+            const float cand = mx - static_cast<float>(13 - ev);
+            const bool up = cand > m_run + kMfTau;  // uniform over the head's lanes
             const float mn = up ? cand : m_run;
             const float al = up ? __builtin_amdgcn_exp2f(m_run - mn) : 1.0f;
             l_run *= al;
