@@ -475,8 +475,8 @@ def main():
         return
 
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the path shards by KV head / sequence without a run here).", file=sys.stderr)
+        print(f"bench.py: the benchmark runs on one GPU; --gpus {args.gpus} is not supported "
+              "(the path would shard by KV head or by sequence; no multi-GPU run is measured).", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

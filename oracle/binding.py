@@ -1,4 +1,4 @@
-"""ctypes bindings for the checker libraries (test infrastructure only).
+"""ctypes bindings for the oracle libraries (test infrastructure only).
 
 Two implementations share one Python surface:
 

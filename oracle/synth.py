@@ -1,4 +1,4 @@
-"""Deterministic synthetic inputs and state digests for the checker (test infrastructure only).
+"""Deterministic synthetic inputs and state digests for the oracle (test infrastructure only).
 
 Inputs come from a counter-based generator of our own (splitmix64 over
 (seed, stream, index)) so fixtures do not depend on numpy's or torch's RNG

@@ -1,7 +1,7 @@
 /*
  * tt_oracle.c -- CPU restatement of TriTierCache's fused decode step.
  *
- * TEST INFRASTRUCTURE ONLY (the checker, never the product). See tt_oracle.h
+ * TEST INFRASTRUCTURE ONLY (the oracle, never the product). See tt_oracle.h
  * for which callers may load it and how each function is pinned.
  *
  * Build: oracle/Makefile, gcc -std=c11 -O2 -ffp-contract=off. The reference's

@@ -1,7 +1,7 @@
 /*
  * tt_oracle.h -- CPU restatement of TriTierCache's fused decode step.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker for the HIP
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle for the HIP
  * implementation in tritiercache_amd/. Only tests/, __graft_entry__.smoke()
  * and bench.py's cpu_baseline leg may load it, and only to check or to time
  * the CPU side. The product path never calls into it.

@@ -1,4 +1,4 @@
-"""Pins the oracle (oracle/tt_oracle.c) before it is trusted as the checker.
+"""Pins the oracle (oracle/tt_oracle.c) before the parity tests trust it.
 
 * the reference's own known-answer vectors (tests/test_quantize_v.cpp,
   tests/tie_test_v.cpp), via tests/golden/*.json;
