@@ -195,6 +195,9 @@ SWEEP = [
     (16, 1, 128, 10, 6, 16, False, "none"),
     (8, 8, 128, 0, 1, 16, False, "none"),
     (7, 1, 128, 0, 3, 16, True, "block"),
+    # two-head groups with 32-token blocks; three KV heads (the plan's uneven branch)
+    (4, 2, 128, 12, 7, 32, True, "holes"),
+    (12, 3, 128, 45, 11, 16, False, "tail"),
 ]
 
 
