@@ -18,6 +18,12 @@ RUNS = {
                                     iv=16, kgs=32, fp16=False, steps=200, prefill=96, seed=12, every=25),
     "step_gqa_d128_fp32": dict(mode="step", Hq=8, Hkv=2, D=128, msl=1024, S=4, R=32, hr=0.05, decay=0.999, iv=32,
                                kgs=16, fp16=False, steps=400, prefill=50, seed=13, every=50),
+    # f16 metadata (the reference engine's default) on the matrix-core path: four-head
+    # groups with 16-token blocks, seven-head groups (padded to eight) with 32-token blocks
+    "step_gqa_d128_fp16": dict(mode="step", Hq=8, Hkv=2, D=128, msl=1024, S=4, R=32, hr=0.05, decay=0.999, iv=32,
+                               kgs=16, fp16=True, steps=300, prefill=64, seed=15, every=50),
+    "step_gqa7_d128_kgs32_fp16": dict(mode="step", Hq=14, Hkv=2, D=128, msl=1024, S=4, R=32, hr=0.05, decay=0.999,
+                                      iv=16, kgs=32, fp16=True, steps=200, prefill=40, seed=16, every=50),
     # long prefill: thresholds over ~36k candidates (the many-workgroup selection on the GPU)
     "step_long_prefill_fp32": dict(mode="step", Hq=4, Hkv=1, D=64, msl=36200, S=4, R=32, hr=0.05, decay=0.999,
                                    iv=32, kgs=16, fp16=False, steps=70, prefill=36000, seed=14, every=32),
