@@ -214,16 +214,32 @@ __device__ __forceinline__ void split_hl4(float a0, float a1, float b0, float b1
     lo = mf_u4{x.y, y.y, z.y, w.y};
 }
 
+// Prefetched metadata stays in its stored width until the pair is laid out:
+// a conversion next to the load would make the prefetch wait for its own data.
+// Four values (K scale or zero of four channels) and one (V scale or zero).
 template <typename MetaT>
-__device__ __forceinline__ float4 load_meta4(const MetaT* __restrict__ p) {
-    if constexpr (sizeof(MetaT) == 4) {
-        return *reinterpret_cast<const float4*>(p);
-    } else {
-        const uint2 v = *reinterpret_cast<const uint2*>(p);
+struct MetaRaw;
+template <>
+struct MetaRaw<float> {
+    using Four = float4;
+    using One = float;
+    __device__ __forceinline__ static Four load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+    __device__ __forceinline__ static One load1(const float* p) { return *p; }
+    __device__ __forceinline__ static float4 f4(const Four v) { return v; }
+    __device__ __forceinline__ static float f1(const One v) { return v; }
+};
+template <>
+struct MetaRaw<uint16_t> {
+    using Four = uint2;
+    using One = uint32_t;
+    __device__ __forceinline__ static Four load4(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
+    __device__ __forceinline__ static One load1(const uint16_t* p) { return *p; }
+    __device__ __forceinline__ static float4 f4(const Four v) {
         return make_float4(f16_to_f32(static_cast<uint16_t>(v.x & 0xffffu)), f16_to_f32(static_cast<uint16_t>(v.x >> 16)),
                            f16_to_f32(static_cast<uint16_t>(v.y & 0xffffu)), f16_to_f32(static_cast<uint16_t>(v.y >> 16)));
     }
-}
+    __device__ __forceinline__ static float f1(const One v) { return f16_to_f32(static_cast<uint16_t>(v)); }
+};
 
 // Even split of `count` items over `parts`: the first item of part `i`
 // (32-bit unsigned arithmetic: count * i stays below 2^32 for every
@@ -582,9 +598,10 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     const PairOffs off_last = pair_offs(min(lane >> 5, Tp - 1 - 2 * (P - 1)), lim_last);
 
     // Registers of the pair being fetched.
+    using MR = MetaRaw<MetaT>;
     mf_u4 kw, vw;
-    float4 ksr, kzr;
-    float vm = 0.0f;
+    typename MR::Four ksr, kzr;
+    typename MR::One vm = 0;
     long long idv = -1;
     bool okv = false;
 
@@ -595,14 +612,14 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         const size_t mb = static_cast<size_t>((W == 2) ? p : 2 * p) * tstride;
         const size_t s0 = static_cast<size_t>(32 * p);
         kw = *reinterpret_cast<const mf_u4*>(at(kp_h + kb, o.k));
-        ksr = load_meta4<MetaT>(reinterpret_cast<const MetaT*>(at(ks_h + mb, o.km)));
-        kzr = load_meta4<MetaT>(reinterpret_cast<const MetaT*>(at(kz_h + mb, o.km)));
+        ksr = MR::load4(reinterpret_cast<const MetaT*>(at(ks_h + mb, o.km)));
+        kzr = MR::load4(reinterpret_cast<const MetaT*>(at(kz_h + mb, o.km)));
         vw = *reinterpret_cast<const mf_u4*>(at(vp_h + s0 * vstride, o.v));
         // V scale in lanes 0-31, V zero in lanes 32-63 (two half-wave loads)
         if (lane < 32)
-            vm = Meta<MetaT>::load(reinterpret_cast<const MetaT*>(at(vs_h + s0 * Hkv, o.vm)), 0);
+            vm = MR::load1(reinterpret_cast<const MetaT*>(at(vs_h + s0 * Hkv, o.vm)));
         else
-            vm = Meta<MetaT>::load(reinterpret_cast<const MetaT*>(at(vz_h + s0 * Hkv, o.vm)), 0);
+            vm = MR::load1(reinterpret_cast<const MetaT*>(at(vz_h + s0 * Hkv, o.vm)));
         idv = *reinterpret_cast<const long long*>(at(in.ids + s0, o.id));
     };
     auto fetch = [&](const int p) {
@@ -699,11 +716,11 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
             vd[g * 4 * kVTS] = y;  // byte column 4 (4 hf + g) + (lane & 3)
         }
         float* kzd = ksz_l + (lane >> 5) * 2 * kKSZ + lk + 4 * ((lane & 31) >> 3);
-        *reinterpret_cast<float4*>(kzd) = ksr;
-        *reinterpret_cast<float4*>(kzd + kKSZ) = kzr;
+        *reinterpret_cast<float4*>(kzd) = MR::f4(ksr);
+        *reinterpret_cast<float4*>(kzd + kKSZ) = MR::f4(kzr);
         const bool ok = okv && idv != -1;
         const int pos = 8 * ((t2 & 15) >> 2) + 4 * (t2 >> 4) + (t2 & 3);
-        (lane < 32 ? vs_l : vz_l)[pos] = ok ? vm : 0.0f;  // masked slots contribute nothing
+        (lane < 32 ? vs_l : vz_l)[pos] = ok ? MR::f1(vm) : 0.0f;  // masked slots contribute nothing
         return static_cast<uint32_t>(__ballot(ok));
     };
 
