@@ -78,8 +78,11 @@ struct MfLds {
     // 128 zero f16 coefficients (a B row that contributes nothing)
     static constexpr int ZERO = QL + GP * kMfD * 4;
     // Per-wave logits of the last LB_PAIRS pairs, [GP][LB_PAIRS * 32] f32: they
-    // reach memory in runs of LB_PAIRS * 128 bytes per head. Eight heads store
-    // their logits directly (buffering them measured slower there).
+    // reach memory in runs of LB_PAIRS * 128 bytes per head, stored early in
+    // the next pair (one wait counter covers loads and stores, so a store issued
+    // late in a pair would hold up the next lay-out). Eight heads store their
+    // logits directly (a buffer of one pair measured 3% slower there: it
+    // spills a register at 168 VGPRs).
     static constexpr int LB_PAIRS = GP > 4 ? 0 : 4;
     static constexpr int LB = ZERO + 256;
     static constexpr int LB_WAVE = GP * LB_PAIRS * 32 * 4;
@@ -755,12 +758,46 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         }
     };
 
-    constexpr int kLbTok = L::LB_PAIRS * 32;  // floats per head in the logits buffer (none: direct stores)
+    constexpr int kLbTok = L::LB_PAIRS * 32;  // floats per head in the logits buffer
     float* lb = reinterpret_cast<float*>(lds + L::LB + wave * L::LB_WAVE);
     int pbuf = wp0;  // first pair held in the logits buffer
+    // Stores the buffered pairs [pbuf, q1) (the caller orders the buffer's LDS
+    // writes first): lane = (head, token quad) with kLbTok / 4 quads per head,
+    // quads past the held pairs idle.
+    auto flush_lb = [&](const int q1) {
+        constexpr int kQuads = kLbTok > 0 ? kLbTok / 4 : 64;  // a power of two
+        constexpr int kHeadsPass = 64 / kQuads;
+        const int qd = lane & (kQuads - 1);
+        const int tok = 32 * pbuf + 4 * qd;
+        if (qd < (q1 - pbuf) * 8) {
+#pragma unroll
+            for (int h0 = 0; h0 < GP; h0 += kHeadsPass) {
+                const int hh = h0 + lane / kQuads;
+                if (hh < gc) {
+                    const float4 v = *reinterpret_cast<const float4*>(lb + hh * kLbTok + 4 * qd);
+                    float* dst = a.logits + static_cast<size_t>(kvh * G + g0 + hh) * a.ld + Nd + tok;
+                    if (tok + 4 <= nslots) {
+                        *reinterpret_cast<float4*>(dst) = v;
+                    } else {
+                        if (tok < nslots) dst[0] = v.x;
+                        if (tok + 1 < nslots) dst[1] = v.y;
+                        if (tok + 2 < nslots) dst[2] = v.z;
+                    }
+                }
+            }
+        }
+    };
     for (int p = wp0; p < wp1; ++p) {
         const uint32_t vmask = stage();
         if (p + 1 < wp1) fetch(p + 1);
+        // the stores go out early in the pair, so they are acknowledged before
+        // the next lay-out waits for the fetch just issued
+        if (L::LB_PAIRS > 0 && a.logits && p - pbuf == L::LB_PAIRS) {
+            wave_lds_sync();
+            flush_lb(p);
+            wave_lds_sync();
+            pbuf = p;
+        }
         wave_lds_sync();
         coeffs(0, 0);
         if (W == 1 && L::NBT == 2) coeffs(1, 1);
@@ -852,7 +889,14 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
                     if (!((vmask >> (16 * tt(i) + 4 * gk + r)) & 1u)) s2[i][r] = kNegInf;
         }
         // The columns of the high parts leave the logits of their head in the
-        // wave's buffer; after LB_PAIRS pairs (or the last) it goes to memory.
+        // wave's buffer (stored when the buffer is full or the loop ends), or
+        // with eight heads in memory directly.
+        if (L::LB_PAIRS > 0 && a.logits && !lo_col && chead < GP) {
+#pragma unroll
+            for (int i = 0; i < NT; ++i)
+                *reinterpret_cast<float4*>(lb + chead * kLbTok + 32 * (p - pbuf) + 16 * tt(i) + 4 * gk) =
+                    make_float4(s2[i][0], s2[i][1], s2[i][2], s2[i][3]);
+        }
         if (L::LB_PAIRS == 0 && a.logits && !lo_col && chead < gc) {
             float* row = a.logits + static_cast<size_t>(kvh * G + g0 + chead) * a.ld + Nd + 32 * p + 4 * gk;
             if (32 * p + 32 <= nslots) {
@@ -866,34 +910,6 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
                         if (32 * p + 16 * tt(i) + 4 * gk + r < nslots) row[16 * tt(i) + r] = s2[i][r];
-            }
-        }
-        if (L::LB_PAIRS > 0 && a.logits) {
-            if (!lo_col && chead < GP) {
-#pragma unroll
-                for (int i = 0; i < NT; ++i)
-                    *reinterpret_cast<float4*>(lb + chead * kLbTok + 32 * (p - pbuf) + 16 * tt(i) + 4 * gk) =
-                        make_float4(s2[i][0], s2[i][1], s2[i][2], s2[i][3]);
-            }
-            if (p - pbuf == L::LB_PAIRS - 1 || p == wp1 - 1) {
-                wave_lds_sync();
-                // lane: token quad `lane` of the buffered pairs, every head of the group
-                if (lane < (p + 1 - pbuf) * 8) {
-                    const int tok = 32 * pbuf + 4 * lane;
-                    for (int hh = 0; hh < gc; ++hh) {
-                        const float4 v = *reinterpret_cast<const float4*>(lb + hh * kLbTok + 4 * lane);
-                        float* dst = a.logits + static_cast<size_t>(kvh * G + g0 + hh) * a.ld + Nd + tok;
-                        if (tok + 4 <= nslots) {
-                            *reinterpret_cast<float4*>(dst) = v;
-                        } else {
-                            if (tok < nslots) dst[0] = v.x;
-                            if (tok + 1 < nslots) dst[1] = v.y;
-                            if (tok + 2 < nslots) dst[2] = v.z;
-                        }
-                    }
-                }
-                wave_lds_sync();
-                pbuf = p + 1;
             }
         }
 
@@ -973,6 +989,10 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         wave_lds_sync();
     }
 
+    if (L::LB_PAIRS > 0 && a.logits && wp1 > pbuf) {
+        wave_lds_sync();
+        flush_lb(wp1);
+    }
     l_run = xrow_sum(l_run);
     pz = xrow_sum(pz);
     if constexpr (TP) {
