@@ -168,3 +168,46 @@ def test_reference_wiring_divergence(C):
     assert np.abs(outs[(16, "fp16")] - outs[(32, "fp16")]).max() > 0
     assert np.abs(outs[(16, "fp16")] - outs[(16, "fp32")]).max() > 0
     del rng
+
+
+def _special_v(V, s, Hkv, D):
+    """Rows of the appended V with the values whose handling depends on the
+    order of the quantiser's min/max fold: NaN, infinities, signed zeros."""
+    V = V.reshape(Hkv, D).copy()
+    k = s % 6
+    if k == 1:
+        V[0, 37] = np.nan
+    elif k == 2:
+        V[0, :] = 0.0
+        V[0, 5::16] = -0.0
+    elif k == 3:
+        V[1 % Hkv, :] = -0.0
+        V[1 % Hkv, 100] = 0.0
+    elif k == 4:
+        V[0, 90] = np.inf
+        V[1 % Hkv, 3] = -np.inf
+    elif k == 5:
+        V[0, ::9] = np.nan
+        V[0, 64] = 0.0
+    return V.reshape(-1).astype(np.float32)
+
+
+@pytest.mark.parametrize("fp16,kgs", [(False, 16), (True, 32)])
+def test_flush_special_values_match_oracle(C, oracle, fp16, kgs):
+    """Waiting-room flushes of V rows holding NaN, +-inf and signed zeros:
+    packed words, scales and zeros equal the oracle's bit for bit."""
+    cfg = dict(mode="inject", Hq=4, Hkv=2, D=128, msl=512, S=4, R=16, hr=0.1, decay=0.999, iv=32, kgs=kgs,
+               fp16=fp16, steps=160, prefill=0, seed=21, every=40)
+    eng = gpu_engine(C, cfg)
+    oe = oracle.engine(*engine_runs.engine_args(cfg))
+    for s in range(cfg["steps"]):
+        _, K, V = engine_runs.step_inputs(cfg, s)
+        V = _special_v(V, s, cfg["Hkv"], cfg["D"])
+        eng.ingest(dev(K), dev(V))
+        oe.ingest(K, V)
+        w = engine_runs.inject_weights(cfg, s, eng.visible())
+        eng.feedback(dev(w))
+        oe.feedback(w)
+        if engine_runs.is_checkpoint(cfg, s):
+            _compare_state(gpu_engine_state(eng), oe.state(), (fp16, kgs, s))
+    assert eng.counters()["pbs_blocks_used"] >= 4

@@ -259,11 +259,15 @@ __device__ void flush_waiting_room(const RouteArgs& a, int blocks) {
                                reinterpret_cast<uint32_t*>(a.kp) + static_cast<size_t>(blocks) * words * kvs + hc,
                                kvs);
     }
-    for (int th = threadIdx.x; th < a.chunk * a.H; th += blockDim.x) {
-        const int t = th / a.H, h = th % a.H;
+    // V rows: one lane per packed word (blockDim is a multiple of D / 16, so
+    // a row's lanes are never split between iterations).
+    const int wpr = a.D / 16;
+    for (int th = threadIdx.x; th < a.chunk * a.H * wpr; th += blockDim.x) {
+        const int r = th / wpr, w = th % wpr;
+        const int t = r / a.H, h = r % a.H;
         const size_t mi = (static_cast<size_t>(blocks) * a.chunk + t) * a.H + h;
-        quant_v_row<MetaT>(a.wr_v + static_cast<size_t>(t) * kvs + static_cast<size_t>(h) * a.D, a.D, vs + mi, vz + mi,
-                           a.vp + mi * (a.D / 16));
+        quant_v_row_lanes<MetaT>(a.wr_v + static_cast<size_t>(t) * kvs + static_cast<size_t>(h) * a.D, w, wpr,
+                                 vs + mi, vz + mi, a.vp + mi * wpr);
     }
     for (int t = threadIdx.x; t < a.chunk; t += blockDim.x)
         a.pbs_ids[static_cast<size_t>(blocks) * a.chunk + t] = a.wr_ids[t];

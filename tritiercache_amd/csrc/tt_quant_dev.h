@@ -90,4 +90,48 @@ __device__ __forceinline__ void quant_v_row(const float* __restrict__ v, int D, 
     }
 }
 
+// quant_v_row with the row's D/16 words over `wpr` = D/16 consecutive lanes
+// of one wave (lane w of the aligned group computes word w). The reference
+// folds the 8-channel chunk minima (maxima) in channel order with a strict
+// compare, so a NaN chunk result never replaces the running value and the
+// first of equal values (a signed zero) stays. Each lane folds its two
+// chunks the same way (never NaN), then the lanes combine in a tree whose
+// kept operand on ties is always the lower channels': the same value as the
+// reference's fold, bit for bit.
+template <typename MetaT>
+__device__ __forceinline__ void quant_v_row_lanes(const float* __restrict__ v, int w, int wpr, MetaT* scale_dst,
+                                                  MetaT* zero_dst, int32_t* packed_dst) {
+    float x[16];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float4 f = reinterpret_cast<const float4*>(v + 16 * w)[j];
+        x[4 * j] = f.x;
+        x[4 * j + 1] = f.y;
+        x[4 * j + 2] = f.z;
+        x[4 * j + 3] = f.w;
+    }
+    float mn = std_min(std_min(__builtin_huge_valf(), hmin8(x)), hmin8(x + 8));
+    float mx = std_max(std_max(-__builtin_huge_valf(), hmax8(x)), hmax8(x + 8));
+    for (int m = 1; m < wpr; m <<= 1) {
+        const float on = __shfl_xor(mn, m, 64), ox = __shfl_xor(mx, m, 64);
+        const bool up = (w & m) != 0;
+        mn = up ? std_min(on, mn) : std_min(mn, on);
+        mx = up ? std_max(ox, mx) : std_max(mx, ox);
+    }
+    const float s = std_max((mx - mn) / 3.0f, 1e-9f);
+    if (w == 0) {
+        Meta<MetaT>::store(scale_dst, 0, s);
+        Meta<MetaT>::store(zero_dst, 0, mn);
+    }
+    uint32_t bits = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        int q = cvt_rne_i32((x[i] - mn) / s);
+        q = q < 3 ? q : 3;
+        q = q > 0 ? q : 0;
+        bits |= static_cast<uint32_t>(q) << (2 * i);
+    }
+    packed_dst[w] = static_cast<int32_t>(bits);
+}
+
 }  // namespace tt
