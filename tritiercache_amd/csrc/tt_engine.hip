@@ -351,23 +351,26 @@ __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
                 bi = i;
             }
         }
-        red_v[tid] = bv;
-        red_i[tid] = bi;
-        __syncthreads();
-        for (int stride = blockDim.x / 2; stride > 0; stride >>= 1) {
-            if (tid < stride) {
-                const float v2 = red_v[tid + stride];
-                const int i2 = red_i[tid + stride];
-                if (i2 >= 0) {
-                    const float v1 = red_v[tid];
-                    const int i1 = red_i[tid];
-                    if (i1 < 0 || v2 < v1 || (v2 == v1 && i2 < i1)) {
-                        red_v[tid] = v2;
-                        red_i[tid] = i2;
-                    }
-                }
+        // (value, index) pairs are ordered by value, then index (a total
+        // order: NaNs were skipped, equal values keep the lower index), so
+        // any combination order gives the scan's result: a butterfly within
+        // each wave, then thread 0 over the waves.
+        auto take = [&](const float v2, const int i2) {
+            if (i2 >= 0 && (bi < 0 || v2 < bv || (v2 == bv && i2 < bi))) {
+                bv = v2;
+                bi = i2;
             }
-            __syncthreads();
+        };
+        for (int m = 32; m > 0; m >>= 1) take(__shfl_xor(bv, m, 64), __shfl_xor(bi, m, 64));
+        if ((tid & 63) == 0) {
+            red_v[tid >> 6] = bv;
+            red_i[tid >> 6] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < static_cast<int>(blockDim.x) / 64; ++w) take(red_v[w], red_i[w]);
+            red_v[0] = bv;
+            red_i[0] = bi;
         }
     }
     if (tid == 0) {
