@@ -10,10 +10,62 @@ namespace tt {
 // token 0 of the channel, tokens `tok_stride` floats apart. `vec` selects the
 // 8-wide vector body semantics (channel < 8*floor(D/8)) versus the scalar tail.
 // Writes scale/zero and kgs/16 words spaced `word_stride` apart.
+// KGS tokens known at compile time: every load is issued before the first
+// use and each value is read once (the runtime-length loop waits for each
+// load in turn, twice).
+template <typename MetaT, int KGS>
+__device__ __forceinline__ void quant_k_channel_n(const float* __restrict__ src, size_t tok_stride, bool vec,
+                                                  MetaT* scale_dst, MetaT* zero_dst, uint32_t* packed_dst,
+                                                  size_t word_stride) {
+    float x[KGS];
+#pragma unroll
+    for (int t = 0; t < KGS; ++t) x[t] = src[t * tok_stride];
+    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+#pragma unroll
+    for (int t = 0; t < KGS; ++t) {
+        if (vec) {
+            mn = x86_minps(mn, x[t]);
+            mx = x86_maxps(mx, x[t]);
+        } else {
+            mn = std_min(mn, x[t]);
+            mx = std_max(mx, x[t]);
+        }
+    }
+    const float d3 = (mx - mn) / 3.0f;
+    const float s = vec ? x86_maxps(d3, 1e-9f) : std_max(d3, 1e-9f);
+    Meta<MetaT>::store(scale_dst, 0, s);
+    Meta<MetaT>::store(zero_dst, 0, mn);
+#pragma unroll
+    for (int w = 0; w < KGS / 16; ++w) {
+        uint32_t bits = 0;
+#pragma unroll
+        for (int st = 0; st < 16; ++st) {
+            int q = cvt_rne_i32((x[w * 16 + st] - mn) / s);
+            if (vec) {
+                q = q > 0 ? q : 0;
+                q = q < 3 ? q : 3;
+            } else {
+                q = q < 3 ? q : 3;
+                q = q > 0 ? q : 0;
+            }
+            bits |= static_cast<uint32_t>(q) << (2 * st);
+        }
+        packed_dst[w * word_stride] = bits;
+    }
+}
+
 template <typename MetaT>
 __device__ __forceinline__ void quant_k_channel(const float* __restrict__ src, size_t tok_stride, int kgs, bool vec,
                                                 MetaT* scale_dst, MetaT* zero_dst, uint32_t* packed_dst,
                                                 size_t word_stride) {
+    if (kgs == 16) {
+        quant_k_channel_n<MetaT, 16>(src, tok_stride, vec, scale_dst, zero_dst, packed_dst, word_stride);
+        return;
+    }
+    if (kgs == 32) {
+        quant_k_channel_n<MetaT, 32>(src, tok_stride, vec, scale_dst, zero_dst, packed_dst, word_stride);
+        return;
+    }
     float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
     for (int t = 0; t < kgs; ++t) {
         const float x = src[t * tok_stride];
