@@ -119,6 +119,24 @@ def test_quantize_v_random_vs_oracle(C, oracle, ch, H, D, fp16):
 
 
 @pytest.mark.parametrize("fp16", [False, True])
+def test_quantize_v_unaligned_rows_vs_oracle(C, oracle, fp16):
+    """V whose rows are only 4-byte aligned (a view one float into its storage)."""
+    ch, H, D = 16, 4, 128
+    V = _edge_values((ch, H, D), 2100)
+    buf = torch.empty(V.size + 1, dtype=torch.float32, device="cuda")
+    Vd = buf[1:].view(ch, H, D)
+    Vd.copy_(torch.from_numpy(V))
+    assert Vd.data_ptr() % 16 == 4
+    mdt, dt = _meta(fp16)
+    p = torch.zeros((ch, H, D // 16), dtype=torch.int32, device="cuda")
+    s = torch.zeros((ch, H), dtype=mdt, device="cuda")
+    z = torch.zeros((ch, H), dtype=mdt, device="cuda")
+    C.quantize_v_block(Vd, p, s, z, H, D, ch, dt)
+    for a, b in zip((host(p), host(s), host(z)), oracle.quantize_v(V, fp16)):
+        assert same_bits(a, b), fp16
+
+
+@pytest.mark.parametrize("fp16", [False, True])
 def test_dequantize_vs_oracle(C, oracle, fp16):
     H, D, nb, kgs = 4, 64, 5, 32
     K = synth.normal(31, 0, (nb * kgs, H, D))

@@ -33,19 +33,22 @@ __global__ void __launch_bounds__(256) quantize_k_kernel(const float* __restrict
                            zero + mi, packed + static_cast<size_t>(ob) * (kgs / 16) * row + hc, row);
 }
 
-// One thread per (token, head). D % 16 == 0 (checked by the host).
+// One lane per packed word of a (token, head) row: D / 16 consecutive lanes
+// per row, their loads coalesced. D % 16 == 0 (checked by the host).
 template <typename MetaT>
 __global__ void __launch_bounds__(256) quantize_v_kernel(const float* __restrict__ V, int32_t* __restrict__ packed,
                                                          MetaT* __restrict__ scale, MetaT* __restrict__ zero,
                                                          int tokens, int H, int D, const int* __restrict__ base_dev,
                                                          int tokens_per_block) {
-    const int th = blockIdx.x * blockDim.x + threadIdx.x;
-    if (th >= tokens * H) return;
-    const int t = th / H, h = th % H;
+    const int wpr = D / 16;  // divides the workgroup, so a row's lanes return together
+    const long long th = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (th >= static_cast<long long>(tokens) * H * wpr) return;
+    const int r = static_cast<int>(th / wpr), w = static_cast<int>(th % wpr);
+    const int t = r / H, h = r % H;
     const int ot = t + (base_dev ? (*base_dev) * tokens_per_block : 0);
     const size_t mi = static_cast<size_t>(ot) * H + h;
-    quant_v_row<MetaT>(V + static_cast<size_t>(t) * H * D + static_cast<size_t>(h) * D, D, scale + mi, zero + mi,
-                       packed + mi * (D / 16));
+    quant_v_row_lanes<MetaT>(V + static_cast<size_t>(t) * H * D + static_cast<size_t>(h) * D, w, wpr, scale + mi,
+                             zero + mi, packed + mi * wpr);
 }
 
 // One thread per (block, head, channel): x = fmaf((float)q, scale, zero).
@@ -108,8 +111,8 @@ int launch_quantize_k(const float* K, uint32_t* packed, void* scale, void* zero,
 int launch_quantize_v(const float* V, int32_t* packed, void* scale, void* zero, int tokens, int H, int D,
                       int meta_fp16, const int* base_dev, int tokens_per_block, hipStream_t stream) {
     if (tokens <= 0 || H <= 0) return TT_OK;
-    const int n = tokens * H;
-    const dim3 grid((n + 255) / 256);
+    const long long n = static_cast<long long>(tokens) * H * (D / 16);
+    const dim3 grid(static_cast<unsigned>((n + 255) / 256));
     if (meta_fp16)
         hipLaunchKernelGGL(quantize_v_kernel<uint16_t>, grid, dim3(256), 0, stream, V, packed,
                            static_cast<uint16_t*>(scale), static_cast<uint16_t*>(zero), tokens, H, D, base_dev,

@@ -113,37 +113,9 @@ __device__ __forceinline__ float hmax8(const float* x) {
 }
 
 // V, one (token, head) row of D channels, D % 16 == 0
-// (quantize_v_avx2.cpp:44-108). Channel 16g+i lands in bits 2i of word g.
-template <typename MetaT>
-__device__ __forceinline__ void quant_v_row(const float* __restrict__ v, int D, MetaT* scale_dst, MetaT* zero_dst,
-                                            int32_t* packed_dst) {
-    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
-    for (int c = 0; c < D; c += 8) {
-        float x[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = v[c + j];
-        mn = std_min(mn, hmin8(x));
-        mx = std_max(mx, hmax8(x));
-    }
-    const float s = std_max((mx - mn) / 3.0f, 1e-9f);
-    Meta<MetaT>::store(scale_dst, 0, s);
-    Meta<MetaT>::store(zero_dst, 0, mn);
-    const int qhd = D / 16;
-    for (int g = 0; g < qhd; ++g) {
-        uint32_t bits = 0;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            int q = cvt_rne_i32((v[g * 16 + i] - mn) / s);
-            q = q < 3 ? q : 3;
-            q = q > 0 ? q : 0;
-            bits |= static_cast<uint32_t>(q) << (2 * i);
-        }
-        packed_dst[g] = static_cast<int32_t>(bits);
-    }
-}
-
-// quant_v_row with the row's D/16 words over `wpr` = D/16 consecutive lanes
-// of one wave (lane w of the aligned group computes word w). The reference
+// (quantize_v_avx2.cpp:44-108): channel 16g+i lands in bits 2i of word g.
+// The row's D/16 words are spread over `wpr` = D/16 consecutive lanes of one
+// wave (lane w of the aligned group computes word w). The reference
 // folds the 8-channel chunk minima (maxima) in channel order with a strict
 // compare, so a NaN chunk result never replaces the running value and the
 // first of equal values (a signed zero) stays. Each lane folds its two
@@ -154,13 +126,18 @@ template <typename MetaT>
 __device__ __forceinline__ void quant_v_row_lanes(const float* __restrict__ v, int w, int wpr, MetaT* scale_dst,
                                                   MetaT* zero_dst, int32_t* packed_dst) {
     float x[16];
+    if ((reinterpret_cast<uintptr_t>(v) & 15) == 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float4 f = reinterpret_cast<const float4*>(v + 16 * w)[j];
-        x[4 * j] = f.x;
-        x[4 * j + 1] = f.y;
-        x[4 * j + 2] = f.z;
-        x[4 * j + 3] = f.w;
+        for (int j = 0; j < 4; ++j) {
+            const float4 f = reinterpret_cast<const float4*>(v + 16 * w)[j];
+            x[4 * j] = f.x;
+            x[4 * j + 1] = f.y;
+            x[4 * j + 2] = f.z;
+            x[4 * j + 3] = f.w;
+        }
+    } else {  // a caller's row that is only 4-byte aligned
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = v[16 * w + i];
     }
     float mn = std_min(std_min(__builtin_huge_valf(), hmin8(x)), hmin8(x + 8));
     float mx = std_max(std_max(-__builtin_huge_valf(), hmax8(x)), hmax8(x + 8));
