@@ -108,7 +108,12 @@ def test_quantize_k_random_vs_oracle(C, oracle, kgs, H, D, fp16):
 
 
 @pytest.mark.parametrize("fp16", [False, True])
-@pytest.mark.parametrize("ch,H,D", [(16, 1, 16), (16, 8, 128), (32, 4, 64), (16, 32, 128), (16, 2, 256)])
+# D / 16 words per row: powers of two, others (48, 80, 96, 112, 160, 192: the
+# row's lane group is padded to a power of two) and more than 64 words
+# (1040, 2048: one thread per row).
+@pytest.mark.parametrize("ch,H,D", [(16, 1, 16), (16, 8, 128), (32, 4, 64), (16, 32, 128), (16, 2, 256),
+                                    (16, 3, 48), (16, 2, 80), (32, 5, 96), (16, 4, 112), (16, 3, 160),
+                                    (16, 2, 192), (16, 2, 1040), (16, 1, 2048)])
 def test_quantize_v_random_vs_oracle(C, oracle, ch, H, D, fp16):
     for seed in range(3):
         V = _edge_values((ch, H, D), 2000 + seed)

@@ -259,14 +259,15 @@ __device__ void flush_waiting_room(const RouteArgs& a, int blocks) {
                                reinterpret_cast<uint32_t*>(a.kp) + static_cast<size_t>(blocks) * words * kvs + hc,
                                kvs);
     }
-    // V rows: one lane per packed word (blockDim is a multiple of D / 16, so
-    // a row's lanes are never split between iterations).
+    // V rows: one lane per packed word. The engine's head_dim is a power of
+    // two of at most 256, so D / 16 lanes form an aligned group that divides
+    // blockDim, and a row's lanes are never split between iterations.
     const int wpr = a.D / 16;
     for (int th = threadIdx.x; th < a.chunk * a.H * wpr; th += blockDim.x) {
         const int r = th / wpr, w = th % wpr;
         const int t = r / a.H, h = r % a.H;
         const size_t mi = (static_cast<size_t>(blocks) * a.chunk + t) * a.H + h;
-        quant_v_row_lanes<MetaT>(a.wr_v + static_cast<size_t>(t) * kvs + static_cast<size_t>(h) * a.D, w, wpr,
+        quant_v_row_lanes<MetaT>(a.wr_v + static_cast<size_t>(t) * kvs + static_cast<size_t>(h) * a.D, w, wpr, wpr,
                                  vs + mi, vz + mi, a.vp + mi * wpr);
     }
     for (int t = threadIdx.x; t < a.chunk; t += blockDim.x)

@@ -33,22 +33,38 @@ __global__ void __launch_bounds__(256) quantize_k_kernel(const float* __restrict
                            zero + mi, packed + static_cast<size_t>(ob) * (kgs / 16) * row + hc, row);
 }
 
-// One lane per packed word of a (token, head) row: D / 16 consecutive lanes
-// per row, their loads coalesced. D % 16 == 0 (checked by the host).
+// One lane per packed word of a (token, head) row: the row's D / 16 words
+// on an aligned group of `group` lanes (a power of two, at most 64, so the
+// group lies in one wave; lanes past D / 16 only pad the min/max tree), the
+// loads of a row coalesced. D % 16 == 0 (checked by the host).
 template <typename MetaT>
 __global__ void __launch_bounds__(256) quantize_v_kernel(const float* __restrict__ V, int32_t* __restrict__ packed,
                                                          MetaT* __restrict__ scale, MetaT* __restrict__ zero,
-                                                         int tokens, int H, int D, const int* __restrict__ base_dev,
-                                                         int tokens_per_block) {
-    const int wpr = D / 16;  // divides the workgroup, so a row's lanes return together
+                                                         int tokens, int H, int D, int group,
+                                                         const int* __restrict__ base_dev, int tokens_per_block) {
+    const int wpr = D / 16;
     const long long th = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (th >= static_cast<long long>(tokens) * H * wpr) return;
-    const int r = static_cast<int>(th / wpr), w = static_cast<int>(th % wpr);
+    // whole groups leave together: the total is a multiple of the group size
+    if (th >= static_cast<long long>(tokens) * H * group) return;
+    const int r = static_cast<int>(th / group), w = static_cast<int>(th % group);
     const int t = r / H, h = r % H;
     const int ot = t + (base_dev ? (*base_dev) * tokens_per_block : 0);
     const size_t mi = static_cast<size_t>(ot) * H + h;
-    quant_v_row_lanes<MetaT>(V + static_cast<size_t>(t) * H * D + static_cast<size_t>(h) * D, w, wpr, scale + mi,
-                             zero + mi, packed + mi * wpr);
+    quant_v_row_lanes<MetaT>(V + static_cast<size_t>(t) * H * D + static_cast<size_t>(h) * D, w, wpr, group,
+                             scale + mi, zero + mi, packed + mi * wpr);
+}
+
+// Rows of more than 64 words (D > 1024): one thread per (token, head) row.
+template <typename MetaT>
+__global__ void __launch_bounds__(256) quantize_v_serial_kernel(const float* __restrict__ V,
+                                                                int32_t* __restrict__ packed,
+                                                                MetaT* __restrict__ scale, MetaT* __restrict__ zero,
+                                                                int tokens, int H, int D) {
+    const int wpr = D / 16;
+    const long long r = static_cast<long long>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (r >= static_cast<long long>(tokens) * H) return;
+    const size_t mi = static_cast<size_t>(r);
+    quant_v_row_serial<MetaT>(V + mi * D, wpr, scale + mi, zero + mi, packed + mi * wpr);
 }
 
 // One thread per (block, head, channel): x = fmaf((float)q, scale, zero).
@@ -111,15 +127,29 @@ int launch_quantize_k(const float* K, uint32_t* packed, void* scale, void* zero,
 int launch_quantize_v(const float* V, int32_t* packed, void* scale, void* zero, int tokens, int H, int D,
                       int meta_fp16, const int* base_dev, int tokens_per_block, hipStream_t stream) {
     if (tokens <= 0 || H <= 0) return TT_OK;
-    const long long n = static_cast<long long>(tokens) * H * (D / 16);
+    const int group = quant_v_group(D / 16);
+    if (group == 0) {
+        if (base_dev) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "quantize_v: head_dim above 1024 in the engine");
+        const long long rows = static_cast<long long>(tokens) * H;
+        const dim3 grid(static_cast<unsigned>((rows + 255) / 256));
+        if (meta_fp16)
+            hipLaunchKernelGGL(quantize_v_serial_kernel<uint16_t>, grid, dim3(256), 0, stream, V, packed,
+                               static_cast<uint16_t*>(scale), static_cast<uint16_t*>(zero), tokens, H, D);
+        else
+            hipLaunchKernelGGL(quantize_v_serial_kernel<float>, grid, dim3(256), 0, stream, V, packed,
+                               static_cast<float*>(scale), static_cast<float*>(zero), tokens, H, D);
+        TT_LAUNCH_CHECK();
+        return TT_OK;
+    }
+    const long long n = static_cast<long long>(tokens) * H * group;
     const dim3 grid(static_cast<unsigned>((n + 255) / 256));
     if (meta_fp16)
         hipLaunchKernelGGL(quantize_v_kernel<uint16_t>, grid, dim3(256), 0, stream, V, packed,
-                           static_cast<uint16_t*>(scale), static_cast<uint16_t*>(zero), tokens, H, D, base_dev,
+                           static_cast<uint16_t*>(scale), static_cast<uint16_t*>(zero), tokens, H, D, group, base_dev,
                            tokens_per_block);
     else
         hipLaunchKernelGGL(quantize_v_kernel<float>, grid, dim3(256), 0, stream, V, packed, static_cast<float*>(scale),
-                           static_cast<float*>(zero), tokens, H, D, base_dev, tokens_per_block);
+                           static_cast<float*>(zero), tokens, H, D, group, base_dev, tokens_per_block);
     TT_LAUNCH_CHECK();
     return TT_OK;
 }

@@ -112,21 +112,41 @@ __device__ __forceinline__ float hmax8(const float* x) {
     return x86_maxps(x86_maxps(m0, m2), x86_maxps(m1, m3));
 }
 
+// Packs 16 channels (x[i] -> bits 2i) against the row's (mn, s).
+__device__ __forceinline__ uint32_t quant_v_word(const float* x, float mn, float s) {
+    uint32_t bits = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        int q = cvt_rne_i32((x[i] - mn) / s);
+        q = q < 3 ? q : 3;
+        q = q > 0 ? q : 0;
+        bits |= static_cast<uint32_t>(q) << (2 * i);
+    }
+    return bits;
+}
+
 // V, one (token, head) row of D channels, D % 16 == 0
 // (quantize_v_avx2.cpp:44-108): channel 16g+i lands in bits 2i of word g.
-// The row's D/16 words are spread over `wpr` = D/16 consecutive lanes of one
-// wave (lane w of the aligned group computes word w). The reference
-// folds the 8-channel chunk minima (maxima) in channel order with a strict
-// compare, so a NaN chunk result never replaces the running value and the
-// first of equal values (a signed zero) stays. Each lane folds its two
-// chunks the same way (never NaN), then the lanes combine in a tree whose
-// kept operand on ties is always the lower channels': the same value as the
-// reference's fold, bit for bit.
+// The row's wpr = D/16 words are spread over a group of `group` consecutive
+// lanes of one wave (group: a power of two, wpr <= group <= 64, so a group
+// never straddles waves); lane w < wpr of the aligned group computes word w,
+// lanes w >= wpr only pad the reduction tree. The reference folds the
+// 8-channel chunk minima (maxima) in channel order with a strict compare, so
+// a NaN chunk result never replaces the running value and the first of equal
+// values (a signed zero) stays. Each lane folds its two chunks the same way
+// (never NaN), then the lanes combine in a tree whose kept operand on ties is
+// always the lower channels': the same value as the reference's fold, bit
+// for bit. Padding lanes hold +inf / -inf, which a real lane's value always
+// keeps (a tie with +inf keeps the lower lane's +inf, the same value).
 template <typename MetaT>
-__device__ __forceinline__ void quant_v_row_lanes(const float* __restrict__ v, int w, int wpr, MetaT* scale_dst,
-                                                  MetaT* zero_dst, int32_t* packed_dst) {
+__device__ __forceinline__ void quant_v_row_lanes(const float* __restrict__ v, int w, int wpr, int group,
+                                                  MetaT* scale_dst, MetaT* zero_dst, int32_t* packed_dst) {
+    const bool real = w < wpr;
     float x[16];
-    if ((reinterpret_cast<uintptr_t>(v) & 15) == 0) {
+    if (!real) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = 0.0f;
+    } else if ((reinterpret_cast<uintptr_t>(v) & 15) == 0) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const float4 f = reinterpret_cast<const float4*>(v + 16 * w)[j];
@@ -139,9 +159,12 @@ __device__ __forceinline__ void quant_v_row_lanes(const float* __restrict__ v, i
 #pragma unroll
         for (int i = 0; i < 16; ++i) x[i] = v[16 * w + i];
     }
-    float mn = std_min(std_min(__builtin_huge_valf(), hmin8(x)), hmin8(x + 8));
-    float mx = std_max(std_max(-__builtin_huge_valf(), hmax8(x)), hmax8(x + 8));
-    for (int m = 1; m < wpr; m <<= 1) {
+    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+    if (real) {
+        mn = std_min(std_min(mn, hmin8(x)), hmin8(x + 8));
+        mx = std_max(std_max(mx, hmax8(x)), hmax8(x + 8));
+    }
+    for (int m = 1; m < group; m <<= 1) {
         const float on = __shfl_xor(mn, m, 64), ox = __shfl_xor(mx, m, 64);
         const bool up = (w & m) != 0;
         mn = up ? std_min(on, mn) : std_min(mn, on);
@@ -152,15 +175,39 @@ __device__ __forceinline__ void quant_v_row_lanes(const float* __restrict__ v, i
         Meta<MetaT>::store(scale_dst, 0, s);
         Meta<MetaT>::store(zero_dst, 0, mn);
     }
-    uint32_t bits = 0;
+    if (real) packed_dst[w] = static_cast<int32_t>(quant_v_word(x, mn, s));
+}
+
+// The same row on one thread, for rows of more than 64 words: the
+// reference's sequential fold over the 8-channel chunks, then every word.
+template <typename MetaT>
+__device__ __forceinline__ void quant_v_row_serial(const float* __restrict__ v, int wpr, MetaT* scale_dst,
+                                                   MetaT* zero_dst, int32_t* packed_dst) {
+    float mn = __builtin_huge_valf(), mx = -__builtin_huge_valf();
+    for (int c = 0; c < 16 * wpr; c += 8) {
+        float x[8];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        int q = cvt_rne_i32((x[i] - mn) / s);
-        q = q < 3 ? q : 3;
-        q = q > 0 ? q : 0;
-        bits |= static_cast<uint32_t>(q) << (2 * i);
+        for (int i = 0; i < 8; ++i) x[i] = v[c + i];
+        mn = std_min(mn, hmin8(x));
+        mx = std_max(mx, hmax8(x));
     }
-    packed_dst[w] = static_cast<int32_t>(bits);
+    const float s = std_max((mx - mn) / 3.0f, 1e-9f);
+    Meta<MetaT>::store(scale_dst, 0, s);
+    Meta<MetaT>::store(zero_dst, 0, mn);
+    for (int w = 0; w < wpr; ++w) {
+        float x[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) x[i] = v[16 * w + i];
+        packed_dst[w] = static_cast<int32_t>(quant_v_word(x, mn, s));
+    }
+}
+
+// Lanes per row for quant_v_row_lanes: the next power of two >= wpr, or 0
+// when that exceeds a wave (use quant_v_row_serial).
+__host__ __device__ inline int quant_v_group(int wpr) {
+    int g = 1;
+    while (g < wpr) g <<= 1;
+    return g <= 64 ? g : 0;
 }
 
 }  // namespace tt
