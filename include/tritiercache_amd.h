@@ -118,6 +118,25 @@ TT_API int tt_fused_attention_decode_ws(const float* Q, const float* dense_K, co
                                  int meta_fp16, void* workspace, size_t workspace_bytes,
                                  void* stream);
 
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the computation of tt_fused_attention_decode, with its
+ * scratch in a static device array of the library (32 MiB, held by every GPU
+ * the library runs on until the process ends) instead of an allocated
+ * workspace. Calls no hipMalloc/hipFree. A call whose workspace would exceed
+ * 32 MiB (tt_fused_attention_workspace_bytes) fails with
+ * TT_ERR_INVALID_ARGUMENT and enqueues nothing. All calls on one GPU share that
+ * GPU's array: calls that overlap on one GPU (other streams, other host
+ * threads) race on it. */
+TT_API int tt_fused_attention_decode_noalloc(const float* Q, const float* dense_K, const float* dense_V,
+                                             int dense_count, const int32_t* PBS_K_Packed,
+                                             const void* PBS_K_Scales, const void* PBS_K_Zeroes,
+                                             const int32_t* PBS_V_Packed, const void* PBS_V_Scales,
+                                             const void* PBS_V_Zeroes, const int64_t* PBS_token_ids,
+                                             int num_blocks, int num_q_heads, int num_kv_heads, int head_dim,
+                                             float* attn_output, float* mean_attn_weights, int k_group_size,
+                                             int meta_fp16, void* stream);
+
 /* The two phases of tt_fused_attention_decode_ws, for callers that merge
  * split-K partials themselves or time the phases separately:
  *   tt_attention_partials  the single-pass split kernel: per (query head,

@@ -49,6 +49,8 @@ _SIGNATURES = {
     "tt_dequantize_v": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "tt_fused_attention_decode": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                                        _vp, _vp, _i, _i, _vp]),
+    "tt_fused_attention_decode_noalloc": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i,
+                                               _i, _vp, _vp, _i, _i, _vp]),
     "tt_fused_attention_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "tt_fused_attention_decode_ws": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i,
                                           _vp, _vp, _i, _i, _vp, _sz, _vp]),

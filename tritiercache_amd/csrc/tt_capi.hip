@@ -47,6 +47,35 @@ int get_workspace(size_t bytes, void** out) {
     return TT_OK;
 }
 
+// Allocation-free workspace: a file-scope device array that every GPU the
+// library runs on holds until the process ends. In host code `scratch` only
+// names the symbol; its device address on the current GPU comes from
+// hipGetSymbolAddress, once per device, and only that address is passed to
+// kernels. Every call on one GPU shares that GPU's copy, so calls that
+// overlap on one GPU race on it.
+constexpr size_t kScratchBytes = static_cast<size_t>(32) << 20;
+__device__ __align__(256) unsigned char scratch[kScratchBytes];
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device.
+int scratch_address(void** out) {
+    int dev = 0;
+    TT_HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxScratchDevices)
+        TT_FAIL(TT_ERR_RUNTIME, "tt_fused_attention_decode_noalloc: device index beyond the scratch table.");
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        TT_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) TT_FAIL(TT_ERR_RUNTIME, "tt_fused_attention_decode_noalloc: no device address for the scratch array.");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return TT_OK;
+}
+
 int check_common(int dense_count, int num_blocks, int Hq, int Hkv, int D, int kgs) {
     if (dense_count < 0) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "dense_count must be non-negative.");
     if (num_blocks < 0) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_blocks must be non-negative.");
@@ -239,6 +268,33 @@ int tt_fused_attention_decode(const float* Q, const float* dense_K, const float*
     return fused_impl(Q, dense_K, dense_V, dense_count, PBS_K_Packed, PBS_K_Scales, PBS_K_Zeroes, PBS_V_Packed,
                       PBS_V_Scales, PBS_V_Zeroes, PBS_token_ids, num_blocks, num_q_heads, num_kv_heads, head_dim,
                       attn_output, mean_attn_weights, k_group_size, meta_fp16, nullptr, 0, true, kBoth, 0,
+                      as_stream(stream));
+}
+
+int tt_fused_attention_decode_noalloc(const float* Q, const float* dense_K, const float* dense_V, int dense_count,
+                                      const int32_t* PBS_K_Packed, const void* PBS_K_Scales, const void* PBS_K_Zeroes,
+                                      const int32_t* PBS_V_Packed, const void* PBS_V_Scales, const void* PBS_V_Zeroes,
+                                      const int64_t* PBS_token_ids, int num_blocks, int num_q_heads, int num_kv_heads,
+                                      int head_dim, float* attn_output, float* mean_attn_weights, int k_group_size,
+                                      int meta_fp16, void* stream) {
+    clear_error();
+    AttnInputs in;
+    AttnPlan plan;
+    int rc = prepare(Q, dense_K, dense_V, dense_count, PBS_K_Packed, PBS_K_Scales, PBS_K_Zeroes, PBS_V_Packed,
+                     PBS_V_Scales, PBS_V_Zeroes, PBS_token_ids, num_blocks, num_q_heads, num_kv_heads, head_dim,
+                     k_group_size, meta_fp16, mean_attn_weights != nullptr, &in, &plan);
+    if (rc) return rc;
+    if (plan.bytes > kScratchBytes)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "tt_fused_attention_decode_noalloc: the call needs " +
+                                             std::to_string(plan.bytes) + " bytes of scratch; the static scratch holds " +
+                                             std::to_string(kScratchBytes) +
+                                             " (use tt_fused_attention_decode_ws with a larger workspace).");
+    void* ws = nullptr;
+    rc = scratch_address(&ws);
+    if (rc) return rc;
+    return fused_impl(Q, dense_K, dense_V, dense_count, PBS_K_Packed, PBS_K_Scales, PBS_K_Zeroes, PBS_V_Packed,
+                      PBS_V_Scales, PBS_V_Zeroes, PBS_token_ids, num_blocks, num_q_heads, num_kv_heads, head_dim,
+                      attn_output, mean_attn_weights, k_group_size, meta_fp16, ws, kScratchBytes, false, kBoth, 0,
                       as_stream(stream));
 }
 
