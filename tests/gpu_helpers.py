@@ -100,3 +100,59 @@ def make_case(oracle, Hq, Hkv, D, nd, nb, kgs, fp16, mask, seed, k_outliers=Fals
     elif mask == "all":
         ids[:] = -1
     return (Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, fp16)
+
+
+def compare_state(g: dict, o: dict, tag) -> None:
+    """Counters and every tier buffer of a GPU engine (gpu_engine_state) equal the
+    oracle engine's (CpuEngine.state()), bit for bit."""
+    assert g["counters"] == o["counters"], (tag, g["counters"], o["counters"])
+    for name in o:
+        if name != "counters":
+            assert same_bits(g[name], o[name].reshape(-1)), (tag, name)
+
+
+def attention_errors(out, ro, mw=None, rmw=None) -> dict:
+    """Errors of a GPU step's output (and mean weights) against the oracle's: the
+    max-normwise error, and the elementwise ratio with 1e-5 max|ref| of absolute
+    slack (the float32 oracle's own sequential sums sit about 1e-6 max|ref| from
+    exact attention, see exact_ref)."""
+    from exact_ref import elementwise_ratio, weights_rel_err
+
+    r = {"norm": rel_err(out, ro), "elem": elementwise_ratio(out, ro, atol_frac=1e-5)}
+    if mw is not None:
+        r["mw_norm"] = rel_err(mw, rmw)
+        r["mw_rel"] = weights_rel_err(mw, rmw)
+    return r
+
+
+def attention_ok(r: dict, tol: float = 1e-4) -> bool:
+    return (r["norm"] <= tol and r["elem"] <= 1.0 and r.get("mw_norm", 0.0) <= tol
+            and r.get("mw_rel", 0.0) <= tol)
+
+
+class Lockstep:
+    """An oracle engine driven beside a GPU engine: the same prefill and step
+    inputs, and after every GPU step the GPU's mean attention weights as the
+    oracle's score feedback (score-injected lockstep). Tier membership, packed
+    words, scales/zeros and scores must then stay bit-identical, while the
+    attention outputs are compared to the tolerance."""
+
+    def __init__(self, oracle, Hq, Hkv, D, msl, S, R, hr, decay, iv, kgs, fp16):
+        self.oe = oracle.engine(Hq, Hkv, D, msl, S, R, hr, decay, iv, kgs, fp16)
+
+    def prefill(self, K, V) -> None:
+        self.oe.prefill(np.ascontiguousarray(K, np.float32), np.ascontiguousarray(V, np.float32))
+
+    def step(self, Q, K, V, out, mw, attend=True):
+        """The oracle's side of one GPU step (host arrays); returns attention_errors
+        of `out` / `mw` when `attend`."""
+        self.oe.ingest(K, V)
+        r = None
+        if attend:
+            ro, rmw = self.oe.attend(Q)
+            r = attention_errors(out, ro, mw, rmw)
+        self.oe.feedback(mw)
+        return r
+
+    def check_state(self, eng, tag) -> None:
+        compare_state(gpu_engine_state(eng), self.oe.state(), tag)

@@ -2,15 +2,22 @@
 tests/test_cache_init.py (TriTierCache construction), tests/test_wiring_verification.py
 (k_group_size / metadata-dtype wiring through _C), tests/test_patch_llama.py and
 tests/test_multi_model_patch.py (the attention patch on tiny offline configs).
-Here every module and tensor lives on the ROCm device and the engine runs on it;
-decode outputs are also checked against float32 attention over the engine's own
-reconstructed tiers.
+Here every module and tensor lives on the ROCm device and the engine runs on it.
+
+TriTierCache.prefill/step and the patched attention of a LLaMA and a Qwen2
+layer (head_dim 128, GQA) also run in score-injected lockstep with the oracle
+engine: the post-RoPE Q/K/V each call hands the engine are fed to the oracle,
+the GPU's mean attention weights are its score feedback, the tier state must
+stay bit-exact and the context vector before o_proj must match the oracle's.
 """
 import math
 
 import numpy as np
 import pytest
 import torch
+
+from gpu_helpers import Lockstep, attention_ok, dev, host
+from oracle import synth
 
 pytestmark = pytest.mark.gpu
 
@@ -200,6 +207,47 @@ def test_decode_matches_attention_over_reconstructed_cache(Hq, Hkv, D, kgs, meta
 
 
 # ---------------------------------------------------------------------------
+# TriTierCache.prefill / step in lockstep with the oracle engine
+# ---------------------------------------------------------------------------
+def _lockstep_for(oracle, cache):
+    from tritiercache_amd.constants import SINK_SIZE, UPDATE_THRESHOLD
+
+    e = cache._engine
+    return Lockstep(oracle, cache.num_q_heads, cache.num_heads, cache.head_dim, cache.max_seq_len, SINK_SIZE,
+                    cache.R_size, cache.H_ratio, cache.score_decay, UPDATE_THRESHOLD, e.k_group_size,
+                    cache.pbs_metadata_dtype == "fp16")
+
+
+@pytest.mark.parametrize("Hq,Hkv,kgs,meta", [(28, 4, 16, "fp32"), (8, 2, 32, "fp16")])
+def test_cache_prefill_and_steps_lockstep_with_oracle(oracle, Hq, Hkv, kgs, meta):
+    """600-token prefill, then 320 decode steps through TriTierCache: past the heavy
+    hitters filling up (41 slots), demotions into the waiting room and flushes."""
+    from tritiercache_amd.cache import TriTierCache
+
+    D, msl, R, hr = 128, 2048, 64, 0.02
+    c = TriTierCache(max_seq_len=msl, head_dim=D, num_heads=Hkv, R_size=R, H_ratio=hr, num_q_heads=Hq,
+                     k_group_size=kgs, pbs_metadata_dtype=meta)
+    ls = _lockstep_for(oracle, c)
+    seed = 300 + Hq
+    Kp, Vp = synth.normal(seed, 1, (600, Hkv, D)), synth.normal(seed, 2, (600, Hkv, D))
+    c.prefill(dev(Kp), dev(Vp))
+    ls.prefill(Kp, Vp)
+    ls.check_state(c._engine, "prefill")
+    blocks0 = c._engine.counters()["pbs_blocks_used"]
+    for s in range(320):
+        q = synth.normal(seed, 10 + 3 * s, (Hq * D,))
+        k, v = synth.normal(seed, 11 + 3 * s, (Hkv * D,)), synth.normal(seed, 12 + 3 * s, (Hkv * D,))
+        out = torch.empty(Hq * D, dtype=torch.float32, device=DEV)
+        c.step(dev(q), dev(k), dev(v), out)
+        r = ls.step(q, k, v, host(out), host(c._engine.get_mean_attn_weights()))
+        assert attention_ok(r), (s, r)
+        if (s + 1) % 40 == 0:
+            ls.check_state(c._engine, s)
+    assert c.HH_count == c.max_heavy_hitters
+    assert c._engine.counters()["pbs_blocks_used"] >= blocks0 + 2
+
+
+# ---------------------------------------------------------------------------
 # HF patch (reference tests/test_patch_llama.py, tests/test_multi_model_patch.py)
 # ---------------------------------------------------------------------------
 transformers = pytest.importorskip("transformers")
@@ -351,3 +399,80 @@ def test_other_architectures_prefill_and_decode(patched, arch):
                                             torch.randn(1, 1, cfg.head_dim, device=DEV, generator=g)))
     assert out.shape == (1, 1, cfg.hidden_size) and torch.isfinite(out).all()
     assert layer.tri_tier_cache.Total_Processed_Tokens == q_len + 1
+
+
+def _spy_lockstep(oracle, cache, every=50):
+    """Wraps the cache's prefill/step so every call the patched layer makes is
+    replayed on the oracle engine (same post-RoPE K/V and Q), with the GPU's mean
+    weights as score feedback; collects the attention errors of each step."""
+    ls = _lockstep_for(oracle, cache)
+    log = {"steps": 0, "errors": []}
+    prefill, step = cache.prefill, cache.step
+
+    def spy_prefill(K, V):
+        prefill(K, V)
+        ls.prefill(host(K.float()), host(V.float()))
+        ls.check_state(cache._engine, "prefill")
+
+    def spy_step(Q, K, V, out):
+        step(Q, K, V, out)
+        r = ls.step(host(Q), host(K), host(V), host(out), host(cache._engine.get_mean_attn_weights()))
+        log["errors"].append(r)
+        log["steps"] += 1
+        if log["steps"] % every == 0:
+            ls.check_state(cache._engine, log["steps"])
+
+    cache.prefill, cache.step = spy_prefill, spy_step
+    return ls, log
+
+
+@pytest.mark.parametrize("arch", ["llama", "qwen2"])
+def test_patched_attention_lockstep_with_oracle(patched, oracle, arch):
+    """A patched LLaMA layer (8 q / 2 KV heads, head_dim 128, the patch's own lazily
+    created cache: 32k capacity, 256-token ring, f16 metadata) and a patched Qwen2
+    layer (14 q / 2 KV heads, head_dim 128, a 1024-token cache set on the module so
+    that its 52 heavy-hitter slots fill and demote): a 700-token prompt, then 300
+    decode steps, each in lockstep with the oracle engine."""
+    import transformers as tf
+
+    from tritiercache_amd.cache import TriTierCache
+
+    torch.manual_seed(5)
+    if arch == "llama":
+        from transformers.models.llama.modeling_llama import LlamaAttention as A, LlamaRotaryEmbedding as Rot
+
+        cfg = tf.LlamaConfig(hidden_size=1024, num_attention_heads=8, num_key_value_heads=2, head_dim=128,
+                             max_position_embeddings=4096)
+    else:
+        from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention as A, Qwen2RotaryEmbedding as Rot
+
+        cfg = tf.Qwen2Config(hidden_size=896, num_attention_heads=14, num_key_value_heads=2, head_dim=128,
+                             max_position_embeddings=4096)
+    layer, rot = A(cfg, layer_idx=0).to(DEV).eval(), Rot(config=cfg).to(DEV)
+    if arch == "qwen2":
+        layer.tri_tier_cache = TriTierCache(max_seq_len=1024, head_dim=128, num_heads=2, R_size=64, H_ratio=0.05,
+                                            num_q_heads=14, score_decay=patched.SCORE_DECAY,
+                                            k_group_size=patched.K_GROUP_SIZE,
+                                            pbs_metadata_dtype=patched.PBS_METADATA_DTYPE)
+    else:
+        # the patch's own cache: create it exactly as the first forward would
+        h0 = torch.randn(1, 1, cfg.hidden_size, device=DEV)
+        patched._layer_cache(layer, h0.device)
+    cache = layer.tri_tier_cache
+    ls, log = _spy_lockstep(oracle, cache)
+    n0 = 700
+    with torch.no_grad():
+        h = torch.randn(1, n0, cfg.hidden_size, device=DEV)
+        layer(h, position_embeddings=rot(h, torch.arange(n0, device=DEV)[None]))
+        for s in range(300):
+            h = torch.randn(1, 1, cfg.hidden_size, device=DEV)
+            out, _ = layer(h, position_embeddings=rot(h, torch.tensor([[n0 + s]], device=DEV)))
+            r = log["errors"][-1]
+            assert attention_ok(r), (arch, s, r)
+    assert log["steps"] == 300 and cache.Total_Processed_Tokens == n0 + 300
+    ls.check_state(cache._engine, "end")
+    worst = {k: max(e[k] for e in log["errors"]) for k in log["errors"][0]}
+    print(arch, "worst over 300 steps", {k: f"{v:.3g}" for k, v in worst.items()}, "hh", cache.HH_count, "blocks",
+          cache._engine.counters()["pbs_blocks_used"], flush=True)
+    if arch == "qwen2":
+        assert cache.HH_count == cache.max_heavy_hitters

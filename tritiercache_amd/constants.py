@@ -1,7 +1,7 @@
 """Constants of the TriTierCache Python API (reference src/tri_tier/constants.py:1-7).
 
-DEVICE is where the Python-side buffers live: the ROCm device when one is
-visible (the engine's tiers are device-resident), else the CPU.
+DEVICE names the device the engine's tiers live on when a GPU is visible
+(the reference uses it for its Python-side buffers).
 """
 import torch
 

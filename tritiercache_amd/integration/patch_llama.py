@@ -1,4 +1,6 @@
-"""Backward-compatible re-exports of the universal patch (reference integration/patch_llama.py)."""
+"""Import path of the reference's LLaMA patcher (src/tri_tier/integration/patch_llama.py),
+kept so callers of ``tri_tier.integration.patch_llama`` find the same functions and
+constants. The patch itself lives in patch_model."""
 from .patch_model import (  # noqa: F401
     H_RATIO,
     HAS_CPP_EXT,
@@ -7,7 +9,6 @@ from .patch_model import (  # noqa: F401
     PBS_METADATA_DTYPE,
     R_SIZE,
     SCORE_DECAY,
-    _reference_attention_path,
     apply_patch,
     is_patched,
     patched_forward,
@@ -15,6 +16,5 @@ from .patch_model import (  # noqa: F401
     reset_caches,
 )
 
-__all__ = ["apply_patch", "remove_patch", "reset_caches", "is_patched", "patched_forward",
-           "_reference_attention_path", "MAX_SEQ_LEN", "R_SIZE", "H_RATIO", "SCORE_DECAY", "K_GROUP_SIZE",
-           "PBS_METADATA_DTYPE", "HAS_CPP_EXT"]
+__all__ = ["apply_patch", "remove_patch", "reset_caches", "is_patched", "patched_forward", "MAX_SEQ_LEN", "R_SIZE",
+           "H_RATIO", "SCORE_DECAY", "K_GROUP_SIZE", "PBS_METADATA_DTYPE", "HAS_CPP_EXT"]

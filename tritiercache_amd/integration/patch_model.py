@@ -1,20 +1,35 @@
-"""HF attention patch for LLaMA / Mistral / Qwen2 / Qwen3 (reference src/tri_tier/integration/patch_model.py).
+"""HF attention patch for the LLaMA, Mistral, Qwen2 and Qwen3 families on the gfx950 engine.
 
-``patched_forward`` replaces the ``forward`` of the supported attention
-classes. Prefill runs SDPA over the prompt and bulk-ingests the prompt's K/V
-into the layer's TriTierCache; decode hands Q and the new K/V to the
-device-resident engine, which runs the fused tiered attention on the GPU.
-Tensors stay on the model's device: on a ROCm model nothing crosses to the
-host (the reference flattens to FP32 CPU tensors, patch_model.py:151-155).
+Public surface of the reference's src/tri_tier/integration/patch_model.py: the
+module constants, ``patched_forward``, ``apply_patch``, ``remove_patch``,
+``reset_caches``, ``is_patched``, ``HAS_CPP_EXT``, the per-module
+``tri_tier_cache`` attribute and the ``capture_needle_pos`` hook.
 
-With output_attentions=True the engine also returns this step's per-head
-attention weights (ordered like the reference's reconstruct_full_cache()).
-Without an engine (CPU-only opt-in mode) the reference's pure-PyTorch path is
-used, as in the reference.
+Design: each patched attention module owns one TriTierCache, created lazily on
+the module's own device. The projections, optional q/k norm and the family's
+rotary embedding (the model file's own ``apply_rotary_pos_emb``) run as in the
+unpatched model; then
+
+* a prompt (q_len > 1) is attended causally with SDPA over its own keys
+  (grouped-query heads shared in place, no repeated K/V) and bulk-ingested into
+  the engine, whose tiers it fills in one prefill launch per tier;
+* a decode token (q_len == 1) goes to the engine as three flat f32 device
+  vectors; the engine's step (ring ingest, routing, packing, fused attention
+  over every tier, score feedback) writes the context vector in device memory,
+  which feeds ``o_proj`` directly. No tensor leaves the device and no step
+  synchronises the host. With output_attentions=True the step also returns the
+  per-head weights over the attended tokens.
+
+There is no path without the engine: a layer whose cache cannot be created
+raises.
 """
+from __future__ import annotations
+
+import sys
 from typing import Any, Dict, List, Optional, Tuple, Type
 
 import torch
+import torch.nn.functional as F
 
 from ..cache import TriTierCache
 
@@ -26,7 +41,6 @@ except ImportError:
     _C = None
     HAS_CPP_EXT = False
 
-
 MAX_SEQ_LEN = 32768
 R_SIZE = 256
 H_RATIO = 0.05
@@ -34,145 +48,126 @@ SCORE_DECAY = 0.999
 K_GROUP_SIZE = 16
 PBS_METADATA_DTYPE = "fp16"
 
-
-def _reference_attention_path(self, cache: TriTierCache, Q: torch.Tensor, num_q_heads: int, num_kv_heads: int,
-                              head_dim: int):
-    """Dense attention over the reconstructed cache (patch_model.py:33-51)."""
-    K_full, V_full, full_ids = cache.reconstruct_full_cache()
-    if num_q_heads != num_kv_heads:
-        rep = num_q_heads // num_kv_heads
-        K_full = K_full.repeat_interleave(rep, dim=1)
-        V_full = V_full.repeat_interleave(rep, dim=1)
-    K_full = K_full.transpose(0, 1).unsqueeze(0).to(dtype=Q.dtype)
-    V_full = V_full.transpose(0, 1).unsqueeze(0).to(dtype=Q.dtype)
-    scaling = getattr(self, "scaling", None) or (head_dim ** -0.5)
-    scores = torch.matmul(Q, K_full.transpose(-2, -1).contiguous()) * scaling
-    weights = torch.softmax(scores, dim=-1)
-    cache.accumulate_attn_scrs(weights, full_ids)
-    return torch.matmul(weights, V_full), weights
+# (modeling module, attention class) of every family the patch serves.
+_FAMILIES = (
+    ("transformers.models.llama.modeling_llama", "LlamaAttention"),
+    ("transformers.models.mistral.modeling_mistral", "MistralAttention"),
+    ("transformers.models.qwen2.modeling_qwen2", "Qwen2Attention"),
+    ("transformers.models.qwen3.modeling_qwen3", "Qwen3Attention"),
+)
 
 
-def _rotate_half(x):
-    half = x.shape[-1] // 2
-    return torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+def _resolve_families() -> List[Type]:
+    found = []
+    for mod, name in _FAMILIES:
+        try:
+            found.append(getattr(__import__(mod, fromlist=[name]), name))
+        except (ImportError, AttributeError):
+            continue
+    return found
+
+
+_SUPPORTED_ATTENTION_CLASSES: List[Type] = _resolve_families()
+_ORIGINAL_FORWARDS: Dict[Type, Any] = {}
+
+
+def _shape(module) -> Tuple[int, int, int]:
+    """(query heads, KV heads, head_dim) of an attention module."""
+    cfg = module.config
+    hq = cfg.num_attention_heads
+    hkv = getattr(cfg, "num_key_value_heads", None) or hq
+    d = getattr(module, "head_dim", None) or cfg.hidden_size // hq
+    return hq, hkv, d
+
+
+def _layer_cache(module, device: torch.device) -> TriTierCache:
+    cache = getattr(module, "tri_tier_cache", None)
+    if cache is None:
+        hq, hkv, d = _shape(module)
+        capacity = max(MAX_SEQ_LEN, getattr(module.config, "max_position_embeddings", MAX_SEQ_LEN))
+        with torch.cuda.device(device):
+            cache = TriTierCache(max_seq_len=capacity, head_dim=d, num_heads=hkv, R_size=R_SIZE, H_ratio=H_RATIO,
+                                 num_q_heads=hq, score_decay=SCORE_DECAY, k_group_size=K_GROUP_SIZE,
+                                 pbs_metadata_dtype=PBS_METADATA_DTYPE)
+        module.tri_tier_cache = cache
+    return cache
+
+
+def _rotated_qkv(module, hidden_states, position_embeddings):
+    """Q [1, Hq, q_len, D], K and V [1, Hkv, q_len, D] after projection, the
+    family's q/k norm (Qwen3) and its rotary embedding."""
+    hq, hkv, d = _shape(module)
+    n = hidden_states.shape[1]
+    q = module.q_proj(hidden_states).view(1, n, hq, d)
+    k = module.k_proj(hidden_states).view(1, n, hkv, d)
+    v = module.v_proj(hidden_states).view(1, n, hkv, d)
+    if getattr(module, "q_norm", None) is not None:
+        q = module.q_norm(q)
+    if getattr(module, "k_norm", None) is not None:
+        k = module.k_norm(k)
+    q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
+    cos, sin = position_embeddings
+    rope = sys.modules[type(module).__module__].apply_rotary_pos_emb
+    q, k = rope(q, k, cos, sin)
+    return q, k, v
 
 
 def patched_forward(self, hidden_states: torch.Tensor,
                     position_embeddings: Optional[Tuple[torch.Tensor, torch.Tensor]] = None,
                     attention_mask: Optional[torch.Tensor] = None, past_key_values: Optional[Any] = None, **kwargs):
-    """Forward of LlamaAttention / MistralAttention / Qwen2Attention / Qwen3Attention."""
+    """Forward of a patched LlamaAttention / MistralAttention / Qwen2Attention / Qwen3Attention.
+    Returns (output, attention weights or None) like the unpatched forward."""
     bsz, q_len, _ = hidden_states.shape
     assert bsz == 1, "TriTierCache only supports batch_size=1"
-
-    num_q_heads = self.config.num_attention_heads
-    num_kv_heads = getattr(self.config, "num_key_value_heads", num_q_heads)
-    head_dim = getattr(self, "head_dim", None) or (self.config.hidden_size // num_q_heads)
-    max_pos = getattr(self.config, "max_position_embeddings", MAX_SEQ_LEN)
-    seq_len_cap = max(MAX_SEQ_LEN, max_pos)
-
-    if getattr(self, "tri_tier_cache", None) is None:
-        self.tri_tier_cache = TriTierCache(
-            max_seq_len=seq_len_cap, head_dim=head_dim, num_heads=num_kv_heads, R_size=R_SIZE, H_ratio=H_RATIO,
-            num_q_heads=num_q_heads, score_decay=SCORE_DECAY, k_group_size=K_GROUP_SIZE,
-            pbs_metadata_dtype=PBS_METADATA_DTYPE)
-    cache = self.tri_tier_cache
-
-    q = self.q_proj(hidden_states).view(bsz, q_len, num_q_heads, head_dim)
-    k = self.k_proj(hidden_states).view(bsz, q_len, num_kv_heads, head_dim)
-    v = self.v_proj(hidden_states).view(bsz, q_len, num_kv_heads, head_dim)
-    if getattr(self, "q_norm", None) is not None:
-        q = self.q_norm(q)
-    if getattr(self, "k_norm", None) is not None:
-        k = self.k_norm(k)
-    Q = q.transpose(1, 2)
-    K_new = k.transpose(1, 2)
-    V_new = v.transpose(1, 2)
-
-    cos, sin = position_embeddings
-    if cos.ndim == 3:
-        cos = cos.unsqueeze(1)
-        sin = sin.unsqueeze(1)
-    Q = (Q * cos) + (_rotate_half(Q) * sin)
-    K_new = (K_new * cos) + (_rotate_half(K_new) * sin)
-
-    need_weights = kwargs.get("output_attentions", False)
+    cache = _layer_cache(self, hidden_states.device)
+    hq, hkv, d = _shape(self)
+    q, k, v = _rotated_qkv(self, hidden_states, position_embeddings)
 
     if q_len > 1:
-        rep = num_q_heads // num_kv_heads
-        K_exp = K_new.repeat_interleave(rep, dim=1) if rep > 1 else K_new
-        V_exp = V_new.repeat_interleave(rep, dim=1) if rep > 1 else V_new
-        ctx = torch.nn.functional.scaled_dot_product_attention(Q, K_exp, V_exp, is_causal=True)
-        K_tokens = K_new.squeeze(0).transpose(0, 1).contiguous()
-        V_tokens = V_new.squeeze(0).transpose(0, 1).contiguous()
-        if getattr(self, "capture_needle_pos", None) is not None:
-            pos = self.capture_needle_pos
-            self.captured_needle_k = K_tokens[pos].clone()
-            self.captured_needle_v = V_tokens[pos].clone()
-        cache.prefill(K_tokens.float(), V_tokens.float())
-        ctx = ctx.transpose(1, 2).reshape(bsz, q_len, -1)
-        return self.o_proj(ctx), None
+        ctx = F.scaled_dot_product_attention(q, k, v, is_causal=True, enable_gqa=hq != hkv)
+        k_tok = k[0].transpose(0, 1).contiguous()  # [q_len, Hkv, D]
+        v_tok = v[0].transpose(0, 1).contiguous()
+        pos = getattr(self, "capture_needle_pos", None)
+        if pos is not None:
+            self.captured_needle_k = k_tok[pos].clone()
+            self.captured_needle_v = v_tok[pos].clone()
+        cache.prefill(k_tok, v_tok)
+        return self.o_proj(ctx.transpose(1, 2).reshape(1, q_len, hq * d)), None
 
-    if cache._engine is not None:
-        Q_flat = Q.reshape(num_q_heads * head_dim).contiguous().float()
-        K_flat = K_new.reshape(num_kv_heads * head_dim).contiguous().float()
-        V_flat = V_new.reshape(num_kv_heads * head_dim).contiguous().float()
-        out = torch.empty((num_q_heads * head_dim,), dtype=torch.float32, device=Q_flat.device)
-        weights = None
-        if need_weights:
-            w, _ = cache.step_with_weights(Q_flat, K_flat, V_flat, out)
-            weights = w.to(Q.device, dtype=Q.dtype).view(1, num_q_heads, 1, -1)
-        else:
-            cache.step(Q_flat, K_flat, V_flat, out)
-        ctx = out.view(bsz, q_len, -1).to(dtype=hidden_states.dtype)
-        return self.o_proj(ctx), weights
-
-    cache.ingest_token(K_new.squeeze(0).squeeze(1).float(), V_new.squeeze(0).squeeze(1).float())
-    ctx, weights = _reference_attention_path(self, cache, Q, num_q_heads, num_kv_heads, head_dim)
-    ctx = ctx.transpose(1, 2).reshape(bsz, q_len, -1).to(dtype=hidden_states.dtype)
-    return self.o_proj(ctx), weights
-
-
-_SUPPORTED_ATTENTION_CLASSES: List[Type] = []
-_ORIGINAL_FORWARDS: Dict[Type, Any] = {}
-_IS_PATCHED: bool = False
-
-for _mod, _cls in (("transformers.models.llama.modeling_llama", "LlamaAttention"),
-                   ("transformers.models.mistral.modeling_mistral", "MistralAttention"),
-                   ("transformers.models.qwen2.modeling_qwen2", "Qwen2Attention"),
-                   ("transformers.models.qwen3.modeling_qwen3", "Qwen3Attention")):
-    try:
-        _SUPPORTED_ATTENTION_CLASSES.append(getattr(__import__(_mod, fromlist=[_cls]), _cls))
-    except (ImportError, AttributeError):
-        pass
+    q_vec = q.reshape(hq * d).float().contiguous()
+    k_vec = k.reshape(hkv * d).float().contiguous()
+    v_vec = v.reshape(hkv * d).float().contiguous()
+    ctx = torch.empty(hq * d, dtype=torch.float32, device=hidden_states.device)
+    weights = None
+    if kwargs.get("output_attentions", False):
+        w, _ = cache.step_with_weights(q_vec, k_vec, v_vec, ctx)
+        weights = w.to(hidden_states.dtype).view(1, hq, 1, -1)
+    else:
+        cache.step(q_vec, k_vec, v_vec, ctx)
+    return self.o_proj(ctx.view(1, 1, hq * d).to(hidden_states.dtype)), weights
 
 
 def apply_patch():
-    """Patch every supported attention class."""
-    global _IS_PATCHED
+    """Route every supported attention class's forward through patched_forward."""
     for cls in _SUPPORTED_ATTENTION_CLASSES:
-        if cls not in _ORIGINAL_FORWARDS:
-            _ORIGINAL_FORWARDS[cls] = cls.forward
+        _ORIGINAL_FORWARDS.setdefault(cls, cls.forward)
         cls.forward = patched_forward
-    _IS_PATCHED = True
 
 
 def remove_patch():
-    """Restore the original forwards."""
-    global _IS_PATCHED
-    for cls, fwd in _ORIGINAL_FORWARDS.items():
-        cls.forward = fwd
-    _IS_PATCHED = False
+    """Restore the forwards apply_patch replaced."""
+    for cls, forward in _ORIGINAL_FORWARDS.items():
+        cls.forward = forward
 
 
 def reset_caches(model):
-    """Drop every lazily created TriTierCache on the model's layers."""
+    """Drop the TriTierCache of every attention module of `model` (a new one is
+    created on the next forward)."""
     for module in model.modules():
         if hasattr(module, "tri_tier_cache"):
             delattr(module, "tri_tier_cache")
 
 
 def is_patched(model_or_module=None) -> bool:
-    """True while the patch is active."""
-    if _IS_PATCHED:
-        return True
-    return any(getattr(cls, "forward", None) == patched_forward for cls in _SUPPORTED_ATTENTION_CLASSES)
+    """True while any supported attention class runs patched_forward."""
+    return any(cls.forward is patched_forward for cls in _SUPPORTED_ATTENTION_CLASSES)
