@@ -199,3 +199,70 @@ def test_engine_matches_reference_digests(oracle, golden, run):
             st = e.state()
             assert synth.state_digest(st["counters"], st) == want["digests"][str(s)], (run, s)
     assert e.counters() == want["final_counters"]
+
+
+# ------------------------------------------------- float64 exact attention helper
+def _tiny_case(oracle, seed):
+    Hq, Hkv, D, nd, nb, kgs = 4, 2, 16, 3, 1, 16
+    Q = synth.normal(seed, 0, (Hq, D))
+    dK, dV = synth.normal(seed, 1, (nd, Hkv, D)), synth.normal(seed, 2, (nd, Hkv, D))
+    KP, KS, KZ = (x[None] for x in oracle.quantize_k(synth.normal(seed, 3, (kgs, Hkv, D)), kgs, False))
+    VP, VS, VZ = oracle.quantize_v(synth.normal(seed, 4, (kgs, Hkv, D)), False)
+    ids = np.arange(kgs, dtype=np.int64) + nd
+    ids[[2, 9]] = -1
+    return (Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, False)
+
+
+def test_exact_attention_helper_brute_force(oracle):
+    """tests/exact_ref.exact_attention (the float64 bar of the GPU tests) against
+    scalar Python loops over the same dequantised values, on a tiny layer with
+    masked slots: equal to 1e-12."""
+    import math
+
+    from exact_ref import exact_attention
+
+    args = _tiny_case(oracle, 41)
+    Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, _ = args
+    out, mw = exact_attention(oracle, *args)
+    K = np.concatenate([dK, oracle.dequantize_k(KP, KS, KZ, nb, Hkv, D, kgs, False)])
+    V = np.concatenate([dV, oracle.dequantize_v(VP, VS, VZ, nb * kgs, Hkv, D, False)])
+    keep = [True] * nd + [bool(i != -1) for i in ids]
+    n = len(keep)
+    want_mw = [0.0] * n
+    for h in range(Hq):
+        kv = h // (Hq // Hkv)
+        s = [sum(float(Q[h, c]) * float(K[t, kv, c]) for c in range(D)) / math.sqrt(D) if keep[t] else None
+             for t in range(n)]
+        m = max(x for x in s if x is not None)
+        e = [math.exp(x - m) if x is not None else 0.0 for x in s]
+        tot = sum(e)
+        for c in range(D):
+            o = sum(e[t] / tot * float(V[t, kv, c]) for t in range(n))
+            assert abs(out[h, c] - o) <= 1e-12 * max(1.0, abs(o))
+        for t in range(n):
+            want_mw[t] += e[t] / tot / Hq
+    assert np.allclose(mw, want_mw, rtol=0, atol=1e-14)
+    assert mw[nd + 2] == 0.0 and mw[nd + 9] == 0.0
+
+
+def test_engine_exact_attention_matches_oracle_engine(oracle):
+    """exact_ref.engine_exact_attention assembles the engine's visible tokens in the
+    engine's order (sinks, heavy hitters, recent window oldest first, packed
+    blocks): its result agrees with the oracle engine's own attention to float32
+    accuracy after a run with a wrapped ring, heavy hitters and flushed blocks."""
+    from exact_ref import elementwise_ratio, engine_exact_attention
+
+    cfg = engine_runs.RUNS["step_gqa_d128_fp16"]
+    e = oracle.engine(*engine_runs.engine_args(cfg))
+    e.prefill(*engine_runs.prefill_inputs(cfg))
+    for s in range(150):
+        Q, K, V = engine_runs.step_inputs(cfg, s)
+        e.step(Q, K, V)
+    Q, K, V = engine_runs.step_inputs(cfg, 150)
+    e.ingest(K, V)
+    c = e.counters()
+    assert c["hh_count"] > 0 and c["pbs_blocks_used"] > 0 and c["rw_head_index"] > 0
+    xo, xmw = engine_exact_attention(oracle, e.state(), Q, cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["kgs"], cfg["fp16"])
+    ro, rmw = e.attend(Q)
+    assert elementwise_ratio(ro, xo.reshape(-1), rtol=1e-5, atol_frac=1e-6) <= 1.0
+    assert np.abs(rmw - xmw).max() <= 1e-6 * xmw.max()

@@ -14,8 +14,12 @@
 //        f16 high part and an f16 low part (two MFMAs, ~22 significant bits),
 //        plus a per-head bias in f32.
 //   PV:  o[h][c] = sum_t p[h][t] (q[t][c] vs[t] + vz[t])
-//              = sum_t (p[h][t] vs[t]) q[t][c] + sum_t p[h][t] vz[t]
-//        A = p vs split hi/lo, B = the 2-bit codes, plus a per-head f32 term.
+//              = sum_t (p[h][t] vs[t] / 2) (2 q[t][c] - 3) + sum_t p[h][t] (vz[t] + 1.5 vs[t])
+//        A = p vs split hi/lo, B = the centred codes 2q - 3, plus a per-head
+//        f32 term. Centring keeps both sums near the size of the output: with
+//        the raw codes they would both grow like the row minimum vz (about
+//        -2.5 for N(0,1) rows, the same sign for every token) and cancel, and
+//        their float32 rounding would dominate the output's error.
 //
 // The 2-bit codes become f16 operands with two instructions per pair of
 // values: the code at bit offset 2k of a byte is masked in place and OR-ed
@@ -172,6 +176,17 @@ __device__ __forceinline__ mf_f4 mfma16x16x32(mf_u4 a, mf_u4 b, mf_f4 c) {
 __device__ __forceinline__ uint32_t code_f16(uint32_t x, uint32_t mk, uint32_t one024) {
     const mf_h2 v = __builtin_bit_cast(mf_h2, (x & mk) | one024);
     const mf_h2 off = {static_cast<_Float16>(1024.0f), static_cast<_Float16>(1024.0f)};
+    return __builtin_bit_cast(uint32_t, v - off);
+}
+
+// Two centred codes: x holds the codes at bit offsets 2k + 1 and 17 + 2k (a
+// word shifted left by one; mk2 selects them) -> the f16 pair
+// ((2 q0 - 3) 4^k, (2 q1 - 3) 4^k), exact: 1024 + 2 q 4^k minus 1024 + 3 4^k
+// (an integer, so the constant and the difference are exact f16 values).
+__device__ __forceinline__ uint32_t code_f16_centred(uint32_t x, uint32_t mk2, uint32_t one024, int k) {
+    const mf_h2 v = __builtin_bit_cast(mf_h2, (x & mk2) | one024);
+    const _Float16 c = static_cast<_Float16>(1024.0f + 3.0f * static_cast<float>(1 << (2 * k)));
+    const mf_h2 off = {c, c};
     return __builtin_bit_cast(uint32_t, v - off);
 }
 
@@ -723,7 +738,12 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         *reinterpret_cast<float4*>(kzd + kKSZ) = MR::f4(kzr);
         const bool ok = okv && idv != -1;
         const int pos = 8 * ((t2 & 15) >> 2) + 4 * (t2 >> 4) + (t2 & 3);
-        (lane < 32 ? vs_l : vz_l)[pos] = ok ? MR::f1(vm) : 0.0f;  // masked slots contribute nothing
+        // lanes 32-63 hold the token's zero, lanes 0-31 its scale: the zero of
+        // the centred codes is vz + 1.5 vs (the middle of the row's range)
+        const float mv = MR::f1(vm);
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mv), __float_as_uint(mv), false, false);
+        const float mc = lane < 32 ? mv : __builtin_fmaf(1.5f, __uint_as_float(sw[0]), mv);
+        (lane < 32 ? vs_l : vz_l)[pos] = ok ? mc : 0.0f;  // masked slots contribute nothing
         return static_cast<uint32_t>(__ballot(ok));
     };
 
@@ -973,17 +993,20 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
                        split_half(pv[NT - 1][1], pv[NT - 1][3], negm_col)};
         }
 
-        // B: codes of channel 4 beta + k for the lane's 8 tokens,
-        // beta = n (nsteps 0..3) and n + 16 (nsteps 4..7), k = nstep & 3.
-        const uint32_t q0a = q0.x >> 8, q0b = q0.y >> 8, q1a = q1.x >> 8, q1b = q1.y >> 8;
+        // B: centred codes of channel 4 beta + k for the lane's 8 tokens,
+        // beta = n (nsteps 0..3) and n + 16 (nsteps 4..7), k = nstep & 3;
+        // bytes 0 and 2 of a word shifted left by one, bytes 1 and 3 shifted
+        // right by seven (the bit shifted into bit 0 is never selected).
+        const uint32_t q0e = q0.x << 1, q0f = q0.y << 1, q1e = q1.x << 1, q1f = q1.y << 1;
+        const uint32_t q0a = q0.x >> 7, q0b = q0.y >> 7, q1a = q1.x >> 7, q1b = q1.y >> 7;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const uint32_t mk = (3u << (2 * k)) | (3u << (16 + 2 * k));
-            const mf_u4 b0 = {code_f16(q0.x, mk, one024), code_f16(q0a, mk, one024), code_f16(q0.y, mk, one024),
-                              code_f16(q0b, mk, one024)};
+            const uint32_t mk2 = (6u << (2 * k)) | (6u << (16 + 2 * k));
+            const mf_u4 b0 = {code_f16_centred(q0e, mk2, one024, k), code_f16_centred(q0a, mk2, one024, k),
+                              code_f16_centred(q0f, mk2, one024, k), code_f16_centred(q0b, mk2, one024, k)};
             acc[k] = mfma16x16x32(ap, b0, acc[k]);
-            const mf_u4 b1 = {code_f16(q1.x, mk, one024), code_f16(q1a, mk, one024), code_f16(q1.y, mk, one024),
-                              code_f16(q1b, mk, one024)};
+            const mf_u4 b1 = {code_f16_centred(q1e, mk2, one024, k), code_f16_centred(q1a, mk2, one024, k),
+                              code_f16_centred(q1f, mk2, one024, k), code_f16_centred(q1b, mk2, one024, k)};
             acc[4 + k] = mfma16x16x32(ap, b1, acc[4 + k]);
         }
         wave_lds_sync();
@@ -1031,7 +1054,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
                 const int h = 4 * gk + r;
                 if (h < GP) {
                     const int c = 4 * n + 64 * (s >> 2) + (s & 3);
-                    sm_acc[(wave * GP + h) * kMfD + c] = __builtin_amdgcn_ldexpf(acc[s][r], -2 * (s & 3));
+                    sm_acc[(wave * GP + h) * kMfD + c] = __builtin_amdgcn_ldexpf(acc[s][r], -2 * (s & 3) - 1);
                 }
             }
     }
