@@ -83,7 +83,9 @@ QK_CASES = [dict(H=2, D=32, kgs=16, fp16=False), dict(H=3, D=64, kgs=32, fp16=Tr
             dict(H=2, D=8, kgs=16, fp16=False), dict(H=1, D=12, kgs=16, fp16=False),
             dict(H=4, D=128, kgs=16, fp16=True)]
 QV_CASES = [dict(H=2, D=32, chunk=16, fp16=False), dict(H=4, D=64, chunk=16, fp16=True),
-            dict(H=1, D=16, chunk=32, fp16=False), dict(H=2, D=128, chunk=16, fp16=True)]
+            dict(H=1, D=16, chunk=32, fp16=False), dict(H=2, D=128, chunk=16, fp16=True),
+            # rows holding NaN, +-inf and signed zeros (the min/max fold order decides them)
+            dict(H=2, D=64, chunk=16, fp16=False, special=True), dict(H=3, D=128, chunk=16, fp16=True, special=True)]
 FA_CASES = [dict(Hq=4, Hkv=2, D=64, nd=20, nb=3, kgs=16, fp16=False, masked=3),
             dict(Hq=8, Hkv=8, D=128, nd=5, nb=7, kgs=16, fp16=True, masked=0),
             dict(Hq=4, Hkv=4, D=16, nd=3, nb=2, kgs=32, fp16=True, masked=5),
@@ -102,6 +104,28 @@ def _special_k(K):
         K[:, 0, 2] = 0.0
         K[::2, 0, 2] = -0.0
     return K
+
+
+def _special_v(V):
+    """Rows of head 0 with the values whose handling depends on the order of the
+    quantiser's min/max fold and conversions: signed zeros, NaN, infinities."""
+    V = V.copy()
+    D = V.shape[2]
+    V[1, 0, :] = 0.0
+    V[1, 0, 5::16] = -0.0
+    V[2, 0, :] = -0.0
+    V[2, 0, D // 2] = 0.0
+    V[3, 0, 37 % D] = np.nan
+    V[4, 0, 9] = np.inf
+    V[5, 0, 3] = -np.inf
+    V[6, 0, ::9] = np.nan
+    V[6, 0, 4] = 0.0
+    V[7, 0, 0] = np.inf
+    V[7, 0, D - 1] = -np.inf
+    V[8, 0, :8] = np.nan      # a whole 8-channel chunk NaN
+    V[9, 0, :] = np.nan       # every channel NaN
+    V[10, 0, 8:16] = -0.0     # a chunk of -0 after a chunk of finite values
+    return V
 
 
 def build_quantized_blocks(R, K, V, kgs, fp16):
@@ -127,6 +151,8 @@ def kernels_small(R):
     for i, c in enumerate(QV_CASES):
         V = synth.normal(200 + i, 0, (c["chunk"], c["H"], c["D"]))
         V[0, 0, :] = 0.75  # constant row -> scale floor
+        if c.get("special"):
+            V = _special_v(V)
         p, s, z = R.quantize_v(V, c["fp16"])
         dq = R.dequantize_v(p, s, z, c["chunk"], c["H"], c["D"], c["fp16"])
         out.update({f"qv{i}_V": V, f"qv{i}_packed": p, f"qv{i}_scale": s, f"qv{i}_zero": z, f"qv{i}_deq": dq})

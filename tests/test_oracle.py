@@ -266,3 +266,27 @@ def test_engine_exact_attention_matches_oracle_engine(oracle):
     ro, rmw = e.attend(Q)
     assert elementwise_ratio(ro, xo.reshape(-1), rtol=1e-5, atol_frac=1e-6) <= 1.0
     assert np.abs(rmw - xmw).max() <= 1e-6 * xmw.max()
+
+
+@pytest.mark.parametrize("fp16,kgs,Hq,Hkv,D,msl,R,hr", [(True, 16, 4, 2, 64, 256, 16, 0.1),
+                                                       (False, 16, 32, 8, 128, 4096, 256, 0.05),
+                                                       (True, 32, 28, 4, 128, 2000, 64, 0.02),
+                                                       (False, 32, 8, 8, 32, 512, 32, 0.3)])
+def test_engine_buffer_bytes_matches_reference(oracle, reference, fp16, kgs, Hq, Hkv, D, msl, R, hr):
+    """The oracle's get_buffer_bytes accounting (cache_engine.cpp:543-568) equals the
+    compiled reference's, before any token, after a prefill that grows the packed
+    store past its first allocation, and after decode steps."""
+    o = oracle.engine(Hq, Hkv, D, msl, 4, R, hr, 0.999, 32, kgs, fp16)
+    r = reference.engine(Hq, Hkv, D, msl, 4, R, hr, 0.999, 32, kgs, fp16)
+    assert o.buffer_bytes() == r.buffer_bytes()
+    n = min(msl - 8, 64 * kgs + 3 * R)
+    K, V = synth.normal(61, 0, (n, Hkv, D)), synth.normal(61, 1, (n, Hkv, D))
+    o.prefill(K, V)
+    r.prefill(K, V)
+    assert o.counters()["pbs_allocated_blocks"] == r.counters()["pbs_allocated_blocks"] > 0
+    assert o.buffer_bytes() == r.buffer_bytes()
+    for s in range(5):
+        q, k, v = synth.normal(62, s, (Hq * D,)), synth.normal(63, s, (Hkv * D,)), synth.normal(64, s, (Hkv * D,))
+        o.step(q, k, v)
+        r.step(q, k, v)
+    assert o.buffer_bytes() == r.buffer_bytes()
