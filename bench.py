@@ -130,15 +130,35 @@ def build_layers(torch, L, Hq, Hkv, D, ctx, layers, outliers, seed, metas=("32",
 PMC_TRAFFIC_MD = os.path.join(ROOT, "profiles", "attn_packed_kernel_llama3-8b-32k_hbm_traffic.md")
 
 
+KERNEL_SOURCES = ("tt_attn.hip", "tt_attn_mfma.h", "tt_attn.h", "tt_common.h")
+
+
+def kernel_source_digest():
+    """SHA-256 (first 16 hex digits) of the attention kernels' sources: stamps a counter summary with the code it
+    measured."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in KERNEL_SOURCES:
+        h.update(open(os.path.join(ROOT, "tritiercache_amd", "csrc", f), "rb").read())
+    return h.hexdigest()[:16]
+
+
 def traffic_from_profile(config, meta):
-    """HBM bytes per partials launch (reads + writes) from the committed counter summary, when it covers this
-    workload and metadata type; None otherwise."""
+    """(HBM bytes per partials launch, reads + writes, from the committed counter summary; whether that summary
+    is stale). The figure is None when the summary does not cover this workload and metadata type, or when it
+    was measured on other kernel sources than the ones built here (then stale is True)."""
     if config != "llama3-8b-32k" or not os.path.exists(PMC_TRAFFIC_MD):
-        return None
+        return None, False
+    stamp, val = None, None
     for line in open(PMC_TRAFFIC_MD):
+        if line.startswith("kernel_sources_sha256:"):
+            stamp = line.split(":")[1].strip()
         if line.startswith(f"traffic_bytes_per_launch[{meta}]:"):
-            return int(line.split(":")[1])
-    return None
+            val = int(line.split(":")[1])
+    if stamp != kernel_source_digest():
+        return None, True
+    return val, False
 
 
 def pmc_driver(torch, lib, L, data, layer_args, tag, fp16, ws, ws_bytes, sp):
@@ -199,6 +219,7 @@ def pmc_summary(dirs):
             wr = med[(k, "WRITE_SIZE")] * wf * 1024
             print(f"{k}: reads {rd / 1e6:.2f} MB, writes {wr / 1e6:.2f} MB per launch\n")
             print(f"traffic_bytes_per_launch[{meta}]: {int(rd + wr)}\n")
+    print(f"kernel_sources_sha256: {kernel_source_digest()}\n")
 
 
 def trace_summary(db_path):
@@ -447,6 +468,43 @@ def batch_bench(args, torch, L, lib):
     print(json.dumps(result), flush=True)
 
 
+def host_cores():
+    """(physical cores, logical CPUs) this process may run on: the affinity mask, cores counted as distinct
+    (socket, core) pairs from lscpu."""
+    import subprocess
+
+    cpus = sorted(os.sched_getaffinity(0))
+    phys = None
+    try:
+        out = subprocess.run(["lscpu", "-p=CPU,CORE,SOCKET"], capture_output=True, text=True, check=True).stdout
+        pairs = {}
+        for line in out.splitlines():
+            if line and not line.startswith("#"):
+                c, core, sock = line.split(",")[:3]
+                pairs[int(c)] = (sock, core)
+        phys = len({pairs[c] for c in cpus if c in pairs}) or None
+    except Exception:
+        pass
+    return phys, len(cpus)
+
+
+def set_omp_threads(n):
+    """Threads of the OpenMP runtime the compiled reference kernel uses (libgomp), for this process."""
+    import ctypes
+
+    try:
+        ctypes.CDLL("libgomp.so.1").omp_set_num_threads(int(n))
+        return True
+    except OSError:
+        return False
+
+
+ARITHMETIC = ("f32 inputs and outputs; FP32 tiers on the VALU in f32; packed tiles on the matrix cores "
+              "(v_mfma_f32_16x16x32_f16, f32 accumulation) with exact f16 2-bit codes (V codes centred, 2q-3) and "
+              "the f32 coefficients Q*k_scale and p*v_scale each split into an f16 high and low part (~22 "
+              "significant bits); softmax in f32 with v_exp_f32")
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -585,11 +643,12 @@ def main():
     step_gbps = bpl * layers / (us_step * 1e-6) / 1e9
     kern_gbps = bpl / (split_us * 1e-6) / 1e9
 
-    # Parity of layer 0 and CPU baseline (reference AVX2+OpenMP kernel on the host cores).
+    # Parity of layer 0 and the CPU baseline: the reference's AVX2+OpenMP kernel on the host cores.
     cpu = None
     parity = None
     if not args.no_cpu:
         from oracle.binding import load_oracle, load_reference
+        from oracle.exact import elementwise_ratio, exact_attention, weights_rel_err
 
         impl = load_reference() or load_oracle()
         d = data[0]
@@ -601,6 +660,8 @@ def main():
         torch.cuda.synchronize()
         gpu_out = data[0]["out"].cpu().numpy()
         gpu_mw = data[0]["mw"].cpu().numpy()
+        phys, logical = host_cores()
+        threads = int(os.environ.get("OMP_NUM_THREADS", 0) or logical) if impl.kind == "reference" else 1
         t1 = time.perf_counter()
         ro, rmw = impl.fused_attention_decode(*cargs)
         first = time.perf_counter() - t1
@@ -611,21 +672,39 @@ def main():
             tot += time.perf_counter() - t1
             n += 1
         per_layer = tot / n
+        one_thread = None
+        if impl.kind == "reference" and threads > 1 and set_omp_threads(1):
+            t1 = time.perf_counter()
+            impl.fused_attention_decode(*cargs)
+            one_thread = time.perf_counter() - t1
+            set_omp_threads(threads)
+        xo, xmw = exact_attention(impl, *cargs)
         parity = {
+            "checked_against": impl.kind,
             "layer0_out_max_rel_err": float(np.abs(gpu_out - ro).max() / np.abs(ro).max()),
             "layer0_mean_weights_max_rel_err": float(np.abs(gpu_mw - rmw).max() / np.abs(rmw).max()),
-            "checked_against": impl.kind,
+            # elementwise: max_i |gpu_i - ref_i| / (1e-4 |ref_i| + a max|ref|), <= 1 passes
+            "layer0_out_elementwise_vs_ref_a1e-5": elementwise_ratio(gpu_out, ro, atol_frac=1e-5),
+            "layer0_out_elementwise_vs_exact_a1e-6": elementwise_ratio(gpu_out, xo),
+            "ref_out_elementwise_vs_exact_a1e-6": elementwise_ratio(ro, xo),
+            "layer0_mean_weights_max_elem_rel_err_vs_ref": weights_rel_err(gpu_mw, rmw),
+            "layer0_mean_weights_max_elem_rel_err_vs_exact": weights_rel_err(gpu_mw, xmw),
+            "exact": "float64 attention over the same dequantised tier values (oracle/exact.py)",
         }
-        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)) if impl.kind == "reference" else 1
         cpu = {
             "value": per_layer * layers * 1e6,
             "unit": "us/step",
             "cores": threads,
+            "physical_cores_available": phys,
+            "logical_cpus_available": logical,
+            "one_thread_us_per_step": None if one_thread is None else one_thread * layers * 1e6,
             "kind": impl.kind,
             "sample": f"{n} calls of one layer ({nd} dense + {nb} blocks, Hq={Hq}, Hkv={Hkv}, D={D}, "
-                      f"{args.meta} metadata, mean weights on), {tot:.1f}s, scaled x{layers} layers",
+                      f"{args.meta} metadata, mean weights on) on {threads} OpenMP threads, {tot:.1f}s, scaled "
+                      f"x{layers} layers; one call on 1 thread, scaled likewise",
         }
 
+    traffic, traffic_stale = traffic_from_profile(args.config, args.meta)
     result = {
         "metric": METRIC,
         "value": round(us_step, 2),
@@ -638,6 +717,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
+        "arithmetic": ARITHMETIC,
         "data": "synthetic (seeded N(0,1) on the GPU, K outlier channels x8; packed by the library quantisers)",
         "config": {
             "workload": f"{args.config}: decode attention over {layers} layers, batch 1, ctx {ctx}, "
@@ -657,7 +737,8 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(kern_gbps / HBM_PEAK_GBPS, 4),
-            "traffic": traffic_from_profile(args.config, args.meta),
+            "traffic": traffic,
+            "traffic_stale": traffic_stale,
             "bytes_per_launch": bpl,
             "avg_launch_us": round(split_us, 3),
         },

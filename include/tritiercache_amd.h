@@ -138,16 +138,25 @@ TT_API int tt_fused_attention_decode_noalloc(const float* Q, const float* dense_
                                              int meta_fp16, void* stream);
 
 /* The two phases of tt_fused_attention_decode_ws, for callers that merge
- * split-K partials themselves or time the phases separately:
+ * split-K partials themselves or overlap the phases:
  *   tt_attention_partials  the single-pass split kernel: per (query head,
  *                          split) running max, sum and weighted V accumulator
  *                          (+ per-token logits when want_mean_weights) into
  *                          `workspace`;
- *   tt_attention_finalize  log-sum-exp merge of the partials -> attn_output,
- *                          and the mean attention weights.
- * Both must be called with the same shape arguments and want_mean_weights;
- * finalize reads only the workspace. No counterpart in the reference, which
- * has a single entry point (bindings.cpp:99-178). */
+ *   tt_attention_finalize  what reads them. With both attn_output and
+ *                          mean_attn_weights: the log-sum-exp merge and the mean
+ *                          attention weights in one launch. With attn_output
+ *                          only: the merge alone, which also leaves each query
+ *                          head's softmax statistics in the workspace. With
+ *                          mean_attn_weights only: the mean weights from those
+ *                          statistics; it must follow a merge-only call on the
+ *                          same workspace and partials (in stream order, or
+ *                          after an event when called on another stream: the
+ *                          mean weights then overlap later work on the first
+ *                          stream, e.g. the next layer's partials).
+ * All calls of one decode step take the same shape arguments and
+ * want_mean_weights. No counterpart in the reference, which has a single entry
+ * point (bindings.cpp:99-178). */
 TT_API int tt_attention_partials(const float* Q, const float* dense_K, const float* dense_V,
                                  int dense_count, const int32_t* PBS_K_Packed,
                                  const void* PBS_K_Scales, const void* PBS_K_Zeroes,

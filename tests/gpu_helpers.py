@@ -115,8 +115,8 @@ def attention_errors(out, ro, mw=None, rmw=None) -> dict:
     """Errors of a GPU step's output (and mean weights) against the oracle's: the
     max-normwise error, and the elementwise ratio with 1e-5 max|ref| of absolute
     slack (the float32 oracle's own sequential sums sit about 1e-6 max|ref| from
-    exact attention, see exact_ref)."""
-    from exact_ref import elementwise_ratio, weights_rel_err
+    exact attention, see oracle.exact)."""
+    from oracle.exact import elementwise_ratio, weights_rel_err
 
     r = {"norm": rel_err(out, ro), "elem": elementwise_ratio(out, ro, atol_frac=1e-5)}
     if mw is not None:

@@ -193,3 +193,66 @@ def test_batched_decode_graph_replays(lib, oracle):
             ro, rmw = oracle.fused_attention_decode(*hargs)
             assert rel_err(host(g_out[i]), ro) <= K.ATTN_TOL, (rep, i)
             assert rel_err(host(g_mw[i]), rmw) <= K.ATTN_TOL, (rep, i)
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,nd,nb,kgs,fp16", [(32, 8, 128, 300, 120, 16, False), (8, 2, 64, 40, 30, 32, True)])
+def test_split_finalize_on_two_streams(lib, oracle, Hq, Hkv, D, nd, nb, kgs, fp16):
+    """tt_attention_partials, a merge-only tt_attention_finalize on the main stream and
+    a mean-weights-only one on a second stream after an event (eagerly, and as one
+    captured graph replayed with new inputs) match tt_fused_attention_decode_ws: the
+    output bit for bit (same merge), the mean weights within 1e-6 (their softmax
+    statistics come from the merge instead of being rebuilt)."""
+    L = lib.load()
+    args = K.make_case(oracle, Hq, Hkv, D, nd, nb, kgs, fp16, "tail", seed=950 + Hq)
+    (Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, fp16) = args
+    t = {k: dev(v) for k, v in dict(Q=Q, dK=dK, dV=dV, KP=KP, KS=KS, KZ=KZ, VP=VP, VS=VS, VZ=VZ, ids=ids).items()}
+    n = nd + nb * kgs
+    ws_bytes = int(L.tt_fused_attention_workspace_bytes(nd, nb, Hq, Hkv, D, kgs, 1))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    side = torch.cuda.Stream()
+    tier = lambda: (t["Q"].data_ptr(), t["dK"].data_ptr(), t["dV"].data_ptr(), nd, t["KP"].data_ptr(),  # noqa: E731
+                    t["KS"].data_ptr(), t["KZ"].data_ptr(), t["VP"].data_ptr(), t["VS"].data_ptr(),
+                    t["VZ"].data_ptr(), t["ids"].data_ptr(), nb, Hq, Hkv, D)
+
+    def fused(out, mw):
+        lib.check(L.tt_fused_attention_decode_ws(*tier(), out.data_ptr(), mw.data_ptr(), kgs, int(fp16),
+                                                 ws.data_ptr(), ws_bytes, _stream()), "fused")
+
+    def split(out, mw):
+        main_s = torch.cuda.current_stream()
+        lib.check(L.tt_attention_partials(*tier(), kgs, int(fp16), 1, ws.data_ptr(), ws_bytes, _stream()), "partials")
+        lib.check(L.tt_attention_finalize(t["Q"].data_ptr(), nd, nb, Hq, Hkv, D, out.data_ptr(), None, kgs, int(fp16),
+                                          1, ws.data_ptr(), ws_bytes, _stream()), "merge")
+        ev = torch.cuda.Event()
+        ev.record(main_s)
+        side.wait_event(ev)
+        lib.check(L.tt_attention_finalize(t["Q"].data_ptr(), nd, nb, Hq, Hkv, D, None, mw.data_ptr(), kgs, int(fp16),
+                                          1, ws.data_ptr(), ws_bytes, C.c_void_p(side.cuda_stream)), "mean")
+        main_s.wait_stream(side)
+
+    def check(out, mw):
+        r_out = torch.empty((Hq, D), device="cuda")
+        r_mw = torch.empty((n,), device="cuda")
+        fused(r_out, r_mw)
+        torch.cuda.synchronize()
+        assert same_bits(host(out), host(r_out))
+        assert np.abs(host(mw) - host(r_mw)).max() <= 1e-6 * np.abs(host(r_mw)).max()
+
+    out = torch.full((Hq, D), float("nan"), device="cuda")
+    mw = torch.full((n,), float("nan"), device="cuda")
+    split(out, mw)
+    torch.cuda.synchronize()
+    check(out, mw)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        split(out, mw)
+    for r in range(3):
+        t["Q"].copy_(dev(synth.normal(960 + r, 0, (Hq, D))))
+        out.fill_(float("nan"))
+        mw.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        check(out, mw)
+    # neither output: rejected
+    assert L.tt_attention_finalize(t["Q"].data_ptr(), nd, nb, Hq, Hkv, D, None, None, kgs, int(fp16), 1,
+                                   ws.data_ptr(), ws_bytes, _stream()) == 1

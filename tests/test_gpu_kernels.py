@@ -3,7 +3,7 @@
 Bar: packed words, scales and zeros bit-exact; attention outputs and mean
 weights within max|gpu - ref| / max|ref| <= 1e-4 (FP32, ATTN_TOL below), and
 on full-size layers also elementwise against float64 attention over the same
-exact tier values (exact_ref).
+exact tier values (oracle.exact).
 """
 import itertools
 
@@ -12,7 +12,7 @@ import pytest
 import torch
 
 from oracle import synth
-from exact_ref import elementwise_ratio, exact_attention, weights_rel_err
+from oracle.exact import elementwise_ratio, exact_attention, weights_rel_err
 from gpu_helpers import dev, host, make_case, quantize_blocks_gpu, rel_err, same_bits
 
 pytestmark = pytest.mark.gpu

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from exact_ref import elementwise_ratio, engine_exact_attention, exact_attention, weights_rel_err
+from oracle.exact import elementwise_ratio, engine_exact_attention, exact_attention, weights_rel_err
 from gpu_helpers import Lockstep, attention_errors, attention_ok, dev, host, rel_err
 from oracle import synth
 

@@ -214,12 +214,12 @@ def _tiny_case(oracle, seed):
 
 
 def test_exact_attention_helper_brute_force(oracle):
-    """tests/exact_ref.exact_attention (the float64 bar of the GPU tests) against
+    """oracle.exact.exact_attention (the float64 bar of the GPU tests) against
     scalar Python loops over the same dequantised values, on a tiny layer with
     masked slots: equal to 1e-12."""
     import math
 
-    from exact_ref import exact_attention
+    from oracle.exact import exact_attention
 
     args = _tiny_case(oracle, 41)
     Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, _ = args
@@ -246,11 +246,11 @@ def test_exact_attention_helper_brute_force(oracle):
 
 
 def test_engine_exact_attention_matches_oracle_engine(oracle):
-    """exact_ref.engine_exact_attention assembles the engine's visible tokens in the
+    """oracle.exact.engine_exact_attention assembles the engine's visible tokens in the
     engine's order (sinks, heavy hitters, recent window oldest first, packed
     blocks): its result agrees with the oracle engine's own attention to float32
     accuracy after a run with a wrapped ring, heavy hitters and flushed blocks."""
-    from exact_ref import elementwise_ratio, engine_exact_attention
+    from oracle.exact import elementwise_ratio, engine_exact_attention
 
     cfg = engine_runs.RUNS["step_gqa_d128_fp16"]
     e = oracle.engine(*engine_runs.engine_args(cfg))

@@ -77,8 +77,15 @@ int attn_launch(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out
 // The two phases of attn_launch: per-split partials (+ logits) into `ws`,
 // then the merge / mean weights / feedback that read them.
 int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipStream_t stream);
+// Which parts of the finalize a launch runs: both in one launch (the merge
+// workgroups next to the mean-weight ones, which rebuild the per-head row
+// statistics themselves), the merge alone (it publishes the row statistics in
+// the workspace), or the mean weights / feedback / per-head weights alone,
+// reading the row statistics a merge-only launch left there.
+enum class FinRoles { kBoth, kMerge, kMean };
 int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out, float* mean_w,
-                         const Feedback* fb, float* head_w, int head_w_ld, hipStream_t stream);
+                         const Feedback* fb, float* head_w, int head_w_ld, hipStream_t stream,
+                         FinRoles roles = FinRoles::kBoth);
 
 // Validates shapes the kernels support.
 int attn_check_shapes(int Hq, int Hkv, int D, int kgs);

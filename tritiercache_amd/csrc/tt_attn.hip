@@ -614,7 +614,7 @@ struct FbToken {
 // MT tokens each. The loads of a block's feedback ids and scores are
 // issued when the block starts, those of the next block's logits as soon as
 // the current ones are consumed.
-template <int MT>
+template <int MT, bool kRowstat>
 __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, float* sh) {
     constexpr int kQuads = MT / 4;         // token quads per block
     constexpr int kGroups = 256 / kQuads;  // head groups per workgroup
@@ -665,7 +665,15 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
     // is not.
     float* Mh = sh;        // [Hq]
     float* iL = sh + Hq;   // [Hq]
-    for (int h0 = 0; h0 < Hq; h0 += 32) {
+    if (kRowstat) {
+        // published by the merge (attn_finalize_kernel's merge role)
+        for (int h = t; h < Hq; h += 256) {
+            const float2 r = *reinterpret_cast<const float2*>(a.rowstat + 2 * h);
+            Mh[h] = r.x;
+            iL[h] = 1.0f / (r.y > 0.0f ? r.y : 1.0f);
+        }
+    }
+    for (int h0 = 0; !kRowstat && h0 < Hq; h0 += 32) {
         const int h = h0 + (t >> 3), j0 = t & 7;
         const float* ml = a.part_ml + static_cast<size_t>(h < Hq ? h : 0) * a.nsplit * 2;
         float mx = kNegInf, ls = 0.0f;
@@ -764,7 +772,15 @@ __global__ void __launch_bounds__(256) attn_finalize_kernel(FinArgs a) {
     if (b < a.Hq)
         fin_merge_head(a, b, sh);
     else
-        fin_mean_tokens<MT>(a, b - a.Hq, static_cast<int>(gridDim.x) - a.Hq, sh);
+        fin_mean_tokens<MT, false>(a, b - a.Hq, static_cast<int>(gridDim.x) - a.Hq, sh);
+}
+
+// The mean-weight role alone, after a merge-only finalize of the same
+// partials: the per-head (M, L) come from the merge's row statistics.
+template <int MT>
+__global__ void __launch_bounds__(256) attn_mean_kernel(FinArgs a) {
+    extern __shared__ float sh[];
+    fin_mean_tokens<MT, true>(a, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -900,7 +916,7 @@ __global__ void __launch_bounds__(256) attn_finalize_batched_kernel(const FinBat
     const int m = blk - merges;
     const int i = batch_find(b.mean_base, b.nseq, m);
     const FinArgs a = fin_batch_args(b, i);
-    fin_mean_tokens<kMeanTokens>(a, m - b.mean_base[i], b.mean_base[i + 1] - b.mean_base[i], sh);
+    fin_mean_tokens<kMeanTokens, false>(a, m - b.mean_base[i], b.mean_base[i + 1] - b.mean_base[i], sh);
 }
 
 template <int CPL, int GP>
@@ -1159,7 +1175,7 @@ int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipS
 }
 
 int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out, float* mean_w,
-                         const Feedback* fb, float* head_w, int head_w_ld, hipStream_t stream) {
+                         const Feedback* fb, float* head_w, int head_w_ld, hipStream_t stream, FinRoles roles) {
     char* base = static_cast<char*>(ws);
     FinArgs f;
     f.part_ml = reinterpret_cast<const float*>(base + plan.off_ml);
@@ -1181,16 +1197,23 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
     f.fb = fb ? *fb : Feedback{};
     const int mt = plan.token_ub >= kMeanLongFrom ? kMeanTokensLong : kMeanTokens;
     int mean_wgs = 0;
-    if (weights) {
+    if (weights && roles != FinRoles::kMerge) {
         const int blocks = (std::max(plan.token_ub, 1) + mt - 1) / mt;
         const int per_wg = (blocks + kMeanMaxWgs - 1) / kMeanMaxWgs;
         mean_wgs = (blocks + per_wg - 1) / per_wg;
     }
     const size_t lds = sizeof(float) * std::max<size_t>(8 + 4 * 256, 2 * static_cast<size_t>(in.Hq) + 256 * 4);
-    if (mt == kMeanTokensLong)
+    if (roles == FinRoles::kMean) {
+        if (mean_wgs == 0) return TT_OK;
+        if (mt == kMeanTokensLong)
+            hipLaunchKernelGGL(attn_mean_kernel<kMeanTokensLong>, dim3(mean_wgs), dim3(256), lds, stream, f);
+        else
+            hipLaunchKernelGGL(attn_mean_kernel<kMeanTokens>, dim3(mean_wgs), dim3(256), lds, stream, f);
+    } else if (mt == kMeanTokensLong) {
         hipLaunchKernelGGL(attn_finalize_kernel<kMeanTokensLong>, dim3(in.Hq + mean_wgs), dim3(256), lds, stream, f);
-    else
+    } else {
         hipLaunchKernelGGL(attn_finalize_kernel<kMeanTokens>, dim3(in.Hq + mean_wgs), dim3(256), lds, stream, f);
+    }
     TT_LAUNCH_CHECK();
     return TT_OK;
 }

@@ -126,7 +126,9 @@ int fused_impl(const float* Q, const float* dK, const float* dV, int dense_count
     int rc = prepare(Q, dK, dV, dense_count, KP, KS, KZ, VP, VS, VZ, ids, num_blocks, Hq, Hkv, D, kgs, meta_fp16,
                      logits, &in, &plan);
     if (rc) return rc;
-    if (phase != kPartials && !out) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'attn_output' pointer address is NULL.");
+    if (phase == kBoth && !out) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'attn_output' pointer address is NULL.");
+    if (phase == kFinalize && !out && !mw)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "tt_attention_finalize: attn_output and mean_attn_weights are both NULL.");
     if (phase == kFinalize && mw && !logits)
         TT_FAIL(TT_ERR_INVALID_ARGUMENT, "mean_attn_weights requested but the partials were planned without them.");
     if (own_ws) {
@@ -136,7 +138,9 @@ int fused_impl(const float* Q, const float* dK, const float* dV, int dense_count
         TT_FAIL(TT_ERR_INVALID_ARGUMENT, "workspace is NULL or smaller than tt_fused_attention_workspace_bytes().");
     }
     if (phase == kPartials) return attn_launch_split(in, plan, ws, s);
-    if (phase == kFinalize) return attn_launch_finalize(in, plan, ws, out, mw, nullptr, nullptr, 0, s);
+    if (phase == kFinalize)
+        return attn_launch_finalize(in, plan, ws, out, mw, nullptr, nullptr, 0, s,
+                                    !mw ? FinRoles::kMerge : (!out ? FinRoles::kMean : FinRoles::kBoth));
     return attn_launch(in, plan, ws, out, mw, nullptr, nullptr, 0, s);
 }
 
