@@ -17,9 +17,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "tritiercache_amd", "csrc")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-# Eight-head groups are held to 168 VGPRs and keep two spilled registers
-# (12 bytes of scratch per lane); every other group size spills nothing.
-LIMITS = {1: 0, 2: 0, 4: 0, 8: 12}
+# No group size spills (eight-head groups are held to 168 VGPRs).
+LIMITS = {1: 0, 2: 0, 4: 0, 8: 0}
 
 
 @pytest.fixture(scope="module")

@@ -402,8 +402,8 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
 // zero and id sit in the same 128-byte lines for all KV heads, so they come
 // from memory once per token instead of once per head.
 //
-// Eight-head groups are held to three waves per SIMD (168 VGPRs; the few
-// spilled values live in the partial-tile logits store).
+// Eight-head groups are held to three waves per SIMD (168 VGPRs, no spills:
+// the loop's rare tail paths and the epilogue recompute their lane indices).
 template <int GP, typename MetaT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GP == 8 ? 3 : 1)))
 attn_packed_kernel(SplitArgs a, const int hc, const int chunks) {

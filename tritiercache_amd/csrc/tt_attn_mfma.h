@@ -925,11 +925,17 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
 #pragma unroll
                     for (int r = 0; r < 4; ++r) row[16 * tt(i) + r] = s2[i][r];
             } else {
+                // the store's last pair (rare): the token offset from an
+                // opaque copy of the thread id, so that no register holds it
+                // over the loop
+                int tx = static_cast<int>(threadIdx.x);
+                asm volatile("" : "+v"(tx));
+                const int t0 = 32 * p + 4 * ((tx >> 4) & 3);
 #pragma unroll
                 for (int i = 0; i < NT; ++i)
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        if (32 * p + 16 * tt(i) + 4 * gk + r < nslots) row[16 * tt(i) + r] = s2[i][r];
+                        if (t0 + 16 * tt(i) + r < nslots) row[16 * tt(i) + r] = s2[i][r];
             }
         }
 
@@ -1041,19 +1047,24 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     float* sm_l = sm_m + 4 * GP;                   // [4][GP]
     float* sm_z = sm_l + 4 * GP;                   // [4][GP]
     float* sm_acc = sm_z + 4 * GP;                 // [4][GP][128]
-    if (lane < GP) {
-        sm_m[wave * GP + lane] = m_run;
-        sm_l[wave * GP + lane] = l_run;
-        sm_z[wave * GP + lane] = pz;
+    // The lane's indices again, from an opaque copy of the thread id: held
+    // over the loop instead, they would cost registers the loop needs.
+    int tx = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(tx));
+    const int lane_e = tx & 63, n_e = tx & 15, gk_e = (tx >> 4) & 3;
+    if (lane_e < GP) {
+        sm_m[wave * GP + lane_e] = m_run;
+        sm_l[wave * GP + lane_e] = l_run;
+        sm_z[wave * GP + lane_e] = pz;
     }
-    if (lane < 32) {
+    if (lane_e < 32) {
 #pragma unroll
         for (int s = 0; s < 8; ++s)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int h = 4 * gk + r;
+                const int h = 4 * gk_e + r;
                 if (h < GP) {
-                    const int c = 4 * n + 64 * (s >> 2) + (s & 3);
+                    const int c = 4 * n_e + 64 * (s >> 2) + (s & 3);
                     sm_acc[(wave * GP + h) * kMfD + c] = __builtin_amdgcn_ldexpf(acc[s][r], -2 * (s & 3) - 1);
                 }
             }

@@ -276,25 +276,54 @@ __device__ void flush_waiting_room(const RouteArgs& a, int blocks) {
 
 // Ring eviction + route_evicted_token (+ flush) for one step, in one
 // workgroup (cache_engine.cpp:414-430, 209-269, 148-207).
+// Order-preserving key of a heavy-hitter score for the argmin: the float's
+// total order in the high word (-0 folded onto +0, which '<' does not tell
+// apart), the slot in the low word, so the smallest key is the first slot
+// of the minimum; NaNs get the largest key and never win.
+__device__ __forceinline__ unsigned long long hh_key(const float v, const int i) {
+    if (v != v) return ~0ull;
+    const unsigned u = __float_as_uint(v + 0.0f);
+    const unsigned o = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<unsigned long long>(o) << 32) | static_cast<unsigned>(i);
+}
+__device__ __forceinline__ unsigned long long wave_min_u64(unsigned long long k) {
+#pragma unroll
+    for (int m = 32; m > 0; m >>= 1) {
+        const unsigned long long o = __shfl_xor(k, m, 64);
+        k = o < k ? o : k;
+    }
+    return k;
+}
+constexpr int kArgminBatch = 8;  // heavy-hitter scores per thread with their loads in flight together
+
 __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
     __shared__ int s_case, s_min_idx;
     __shared__ float s_score;
-    __shared__ float red_v[1024];
-    __shared__ int red_i[1024];
+    __shared__ unsigned long long red_k[16];
     const int tid = threadIdx.x;
     const int kvs = a.kvs;
     int* st = a.st;
     const int hh = st[kHhCount];
     const int wr = st[kWrCount];
+    const int blocks = st[kBlocksUsed];
+    const int evictions = st[kTotalEvictions], total = st[kTotal];
+    const int logical = st[kLogicalAlloc], pbs_count = st[kPbsCount];
+
+    // Score and threshold (cache_engine.cpp:216-218).
+    const long long eid = a.evicted_id;
+    const float score = (eid >= 0 && eid < a.max_seq_len) ? a.g[eid] : 0.0f;
+    const float thr = a.thr_zero ? 0.0f : __int_as_float(st[kThreshold]);
 
     // Evicted row out of the ring slot, new token in (each thread owns the
     // same elements for the read and the write). Rows of up to
     // 1024 kRouteRegs elements stay in registers until they are written to
-    // their tier; longer rows go through the EV buffers.
+    // their tier; longer rows go through the EV buffers. The loads of the
+    // exchange, the scores of the argmin below and the score / threshold
+    // above all go out before the first store.
     float* rk = a.rw_k + static_cast<size_t>(a.slot) * kvs;
     float* rv = a.rw_v + static_cast<size_t>(a.slot) * kvs;
     const bool in_regs = kvs <= 1024 * kRouteRegs;
-    float evk[kRouteRegs], evv[kRouteRegs];
+    float evk[kRouteRegs], evv[kRouteRegs], kn[kRouteRegs], vn[kRouteRegs];
     if (in_regs) {
 #pragma unroll
         for (int j = 0; j < kRouteRegs; ++j) {
@@ -302,8 +331,46 @@ __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
             if (e < kvs) {
                 evk[j] = rk[e];
                 evv[j] = rv[e];
-                rk[e] = a.k_new[e];
-                rv[e] = a.v_new[e];
+                kn[j] = a.k_new[e];
+                vn[j] = a.v_new[e];
+            }
+        }
+    }
+
+    // Argmin over HH_scores[0..hh) with the sequential scan's semantics
+    // (cache_engine.cpp:224-232): first index of the minimum under '<'; NaNs
+    // never win unless at slot 0, which the decision below handles. Each
+    // thread keeps kArgminBatch loads in flight, then a min over the keys.
+    // It runs whenever the heavy hitters are full, whatever the score, so
+    // that its loads go out with the others (the decision reads it only
+    // when the score passes the threshold).
+    const bool need_min = (hh >= a.max_hh) && hh > 0;
+    float h0 = 0.0f;  // slot 0's score, read by the decision
+    if (tid == 0 && hh >= a.max_hh) h0 = a.hh_scores[0];
+    unsigned long long best = ~0ull;
+    if (need_min) {
+        for (int i0 = 0; i0 < hh; i0 += 1024 * kArgminBatch) {
+            float v[kArgminBatch];
+#pragma unroll
+            for (int u = 0; u < kArgminBatch; ++u) {
+                const int i = i0 + tid + 1024 * u;
+                v[u] = i < hh ? a.hh_scores[i] : __int_as_float(0x7fc00000);
+            }
+#pragma unroll
+            for (int u = 0; u < kArgminBatch; ++u) {
+                const unsigned long long k = hh_key(v[u], i0 + tid + 1024 * u);
+                best = k < best ? k : best;
+            }
+        }
+    }
+
+    if (in_regs) {
+#pragma unroll
+        for (int j = 0; j < kRouteRegs; ++j) {
+            const int e = tid + 1024 * j;
+            if (e < kvs) {
+                rk[e] = kn[j];
+                rv[e] = vn[j];
             }
         }
     } else {
@@ -312,6 +379,15 @@ __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
             a.ev_v[e] = rv[e];
             rk[e] = a.k_new[e];
             rv[e] = a.v_new[e];
+        }
+    }
+    if (need_min) {
+        best = wave_min_u64(best);
+        if ((tid & 63) == 0) red_k[tid >> 6] = best;
+        __syncthreads();
+        if (tid < 64) {
+            best = wave_min_u64(tid < static_cast<int>(blockDim.x >> 6) ? red_k[tid] : ~0ull);
+            if (tid == 0) red_k[0] = best;
         }
     }
     // The evicted row into `dk` / `dv` (row layout [kvs]).
@@ -333,61 +409,23 @@ __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
         }
     };
 
-    // Score and threshold (cache_engine.cpp:216-218).
-    const long long eid = a.evicted_id;
-    const float score = (eid >= 0 && eid < a.max_seq_len) ? a.g[eid] : 0.0f;
-    const float thr = a.thr_zero ? 0.0f : __int_as_float(st[kThreshold]);
-
-    // Argmin over HH_scores[0..hh) with the sequential scan's semantics:
-    // first index of the minimum under '<' (NaNs never win unless at slot 0).
-    const bool need_min = (score >= thr) && (hh >= a.max_hh) && hh > 0;
-    if (need_min) {
-        float bv = 0.0f;
-        int bi = -1;
-        for (int i = tid; i < hh; i += blockDim.x) {
-            const float v = a.hh_scores[i];
-            if (v != v) continue;
-            if (bi < 0 || v < bv) {
-                bv = v;
-                bi = i;
-            }
-        }
-        // (value, index) pairs are ordered by value, then index (a total
-        // order: NaNs were skipped, equal values keep the lower index), so
-        // any combination order gives the scan's result: a butterfly within
-        // each wave, then thread 0 over the waves.
-        auto take = [&](const float v2, const int i2) {
-            if (i2 >= 0 && (bi < 0 || v2 < bv || (v2 == bv && i2 < bi))) {
-                bv = v2;
-                bi = i2;
-            }
-        };
-        for (int m = 32; m > 0; m >>= 1) take(__shfl_xor(bv, m, 64), __shfl_xor(bi, m, 64));
-        if ((tid & 63) == 0) {
-            red_v[tid >> 6] = bv;
-            red_i[tid >> 6] = bi;
-        }
-        __syncthreads();
-        if (tid == 0) {
-            for (int w = 1; w < static_cast<int>(blockDim.x) / 64; ++w) take(red_v[w], red_i[w]);
-            red_v[0] = bv;
-            red_i[0] = bi;
-        }
-    }
     if (tid == 0) {
         int c = kToWR, mi = 0;
         if (score >= thr) {
             if (hh < a.max_hh) {
                 c = kToHH;
             } else {
-                const float h0 = a.hh_scores[0];
                 float mv;
-                if (h0 != h0 || red_i[0] < 0) {
+                const unsigned long long best = need_min ? red_k[0] : ~0ull;
+                if (h0 != h0 || best == ~0ull) {
                     mi = 0;
                     mv = h0;
                 } else {
-                    mi = red_i[0];
-                    mv = red_v[0];
+                    // the value back from its key (a zero comes back as +0,
+                    // which compares like -0)
+                    mi = static_cast<int>(best & 0xffffffffu);
+                    const unsigned o = static_cast<unsigned>(best >> 32);
+                    mv = __uint_as_float((o & 0x80000000u) ? (o & 0x7fffffffu) : ~o);
                 }
                 if (score > mv) c = kReplace;
             }
@@ -413,8 +451,9 @@ __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
         float* wk = a.wr_k + static_cast<size_t>(wr) * kvs;
         float* wv = a.wr_v + static_cast<size_t>(wr) * kvs;
         for (int e = tid; e < kvs; e += blockDim.x) {
-            wk[e] = hk[e];
-            wv[e] = hv[e];
+            const float x = hk[e], y = hv[e];  // both loads before either store
+            wk[e] = x;
+            wv[e] = y;
         }
         put_evicted(hk, hv);  // each thread overwrites only elements it has read
         if (tid == 0) {
@@ -428,30 +467,29 @@ __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
     }
     const int new_hh = hh + (c == kToHH ? 1 : 0);
     const int new_wr = wr + (c == kToHH ? 0 : 1);
-    __syncthreads();
 
-    int blocks = st[kBlocksUsed];
-    if (new_wr == a.chunk) {
-        if (a.fp16)
-            flush_waiting_room<uint16_t>(a, blocks);
-        else
-            flush_waiting_room<float>(a, blocks);
-    }
-    __syncthreads();
+    // The counters (read at the start, written by thread 0 only) need no
+    // barrier; the flush reads waiting-room rows other threads just wrote.
     if (tid == 0) {
         st[kHhCount] = new_hh;
-        st[kTotalEvictions] += 1;
+        st[kTotalEvictions] = evictions + 1;
         st[kRwHead] = a.new_head;
-        st[kTotal] += 1;
+        st[kTotal] = total + 1;
         if (new_wr == a.chunk) {
-            const int la = st[kLogicalAlloc];
-            if (blocks + 1 > la) st[kLogicalAlloc] = max(la + 64, blocks + 1);
+            if (blocks + 1 > logical) st[kLogicalAlloc] = max(logical + 64, blocks + 1);
             st[kBlocksUsed] = blocks + 1;
-            st[kPbsCount] += a.chunk;
+            st[kPbsCount] = pbs_count + a.chunk;
             st[kWrCount] = 0;
         } else {
             st[kWrCount] = new_wr;
         }
+    }
+    if (new_wr == a.chunk) {  // uniform
+        __syncthreads();
+        if (a.fp16)
+            flush_waiting_room<uint16_t>(a, blocks);
+        else
+            flush_waiting_room<float>(a, blocks);
     }
 }
 
