@@ -56,13 +56,18 @@ constexpr float kMfTau = 2.0f;  // slack of the lazy rescale, log2 units
 // padded so that the wide LDS accesses of one instruction (8 lanes x 16
 // bytes, 16 lanes x 8 bytes) fall into distinct banks.
 constexpr int kKTS = 36;   // dwords per K row (token quad): 128 channel bytes + 4 dwords pad
-constexpr int kVTS = 10;   // dwords per V byte column: 32 token bytes + 2 dwords pad
+// V byte column r (32 token bytes = 8 dwords, in MFMA order) starts at dword
+// 8 r + (r >> 4) with its dwords permuted by XOR 2 ((r >> 2) & 3): the lay-out
+// writes (16 lanes of 4 bytes per cycle) and the operand reads (16 lanes of
+// 8 bytes) then each fall into 32 distinct banks; columns 16..31 start at an
+// odd dword, so their 8-byte reads are two 4-byte reads.
+__device__ __forceinline__ int vt_dword(const int r, const int d) { return 8 * r + (r >> 4) + (d ^ (2 * ((r >> 2) & 3))); }
 constexpr int kKSZ = 144;  // floats per K scale (zero) row: channel c at c + 4 (c / 32)
 constexpr int kBRS = 136;  // halves per coefficient row: 128 + 8 pad
 template <int GP>
 struct MfLds {
     static constexpr int KT = 0;       // [2 tiles][4 token quads][kKTS dwords]
-    static constexpr int VT = 1152;    // [32 byte columns][kVTS dwords], token bytes in MFMA order
+    static constexpr int VT = 1152;    // [32 byte columns][8 dwords] + 1 (vt_dword), token bytes in MFMA order
     static constexpr int KSZ = 2432;   // [2 tiles][scale | zero][kKSZ] f32
     static constexpr int VS = 4736;    // [32] f32, MFMA token order (0 for masked slots)
     static constexpr int VZ = 4864;    // [32] f32
@@ -77,11 +82,13 @@ struct MfLds {
     // final merge of the four waves, reusing the staging area
     static constexpr int MERGE = 4 * GP * (3 + kMfD) * 4;
     static_assert(MERGE <= 4 * BYTES, "merge area must fit in the staging area");
+    static_assert(VT + 4 * (8 * 31 + 1 + 7 + 1) <= KSZ, "V byte columns must fit before the K scales");
     // the workgroup's query heads [GP][128] f32, after the four staging areas
     static constexpr int QL = 4 * BYTES;
     // 128 zero f16 coefficients (a B row that contributes nothing)
     static constexpr int ZERO = QL + GP * kMfD * 4;
-    // Per-wave logits of the last LB_PAIRS pairs, [GP][LB_PAIRS * 32] f32: they
+    // Per-wave logits of the last LB_PAIRS pairs, [GP][LB_PAIRS * 32 + 4] f32 (the
+    // 4 floats of padding put the heads' 16-byte writes in distinct banks): they
     // reach memory in runs of LB_PAIRS * 128 bytes per head, stored early in
     // the next pair (one wait counter covers loads and stores, so a store issued
     // late in a pair would hold up the next lay-out). Eight heads store their
@@ -89,7 +96,8 @@ struct MfLds {
     // spills a register at 168 VGPRs).
     static constexpr int LB_PAIRS = GP > 4 ? 0 : 4;
     static constexpr int LB = ZERO + 256;
-    static constexpr int LB_WAVE = GP * LB_PAIRS * 32 * 4;
+    static constexpr int LB_HEAD = LB_PAIRS > 0 ? LB_PAIRS * 32 + 4 : 0;  // floats per head
+    static constexpr int LB_WAVE = GP * LB_HEAD * 4;
     static constexpr int TOTAL = LB + 4 * LB_WAVE;
 };
 
@@ -724,14 +732,14 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         // V: 4x4 byte transpose across the quad (tokens 4m..4m+3).
         const int m = lane >> 3;
         const int hf = (lane >> 2) & 1;
-        uint32_t* vd = vt_l + (16 * hf + (lane & 3)) * kVTS + 2 * (m & 3) + (m >> 2);
         const uint32_t vwv[4] = {vw.x, vw.y, vw.z, vw.w};
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const uint32_t x = vwv[g];
             const uint32_t t = __builtin_amdgcn_perm(dpp_u32_quad1(x), x, qsel1);
             const uint32_t y = __builtin_amdgcn_perm(dpp_u32_quad2(t), t, qsel2);
-            vd[g * 4 * kVTS] = y;  // byte column 4 (4 hf + g) + (lane & 3)
+            // byte column 4 (4 hf + g) + (lane & 3), token-quad dword 2 (m & 3) + (m >> 2)
+            vt_l[vt_dword(16 * hf + 4 * g + (lane & 3), 2 * (m & 3) + (m >> 2))] = y;
         }
         float* kzd = ksz_l + (lane >> 5) * 2 * kKSZ + lk + 4 * ((lane & 31) >> 3);
         *reinterpret_cast<float4*>(kzd) = MR::f4(ksr);
@@ -778,7 +786,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         }
     };
 
-    constexpr int kLbTok = L::LB_PAIRS * 32;  // floats per head in the logits buffer
+    constexpr int kLbTok = L::LB_PAIRS * 32;  // logits per head in the buffer (rows of L::LB_HEAD floats)
     float* lb = reinterpret_cast<float*>(lds + L::LB + wave * L::LB_WAVE);
     int pbuf = wp0;  // first pair held in the logits buffer
     // Stores the buffered pairs [pbuf, q1) (the caller orders the buffer's LDS
@@ -794,7 +802,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
             for (int h0 = 0; h0 < GP; h0 += kHeadsPass) {
                 const int hh = h0 + lane / kQuads;
                 if (hh < gc) {
-                    const float4 v = *reinterpret_cast<const float4*>(lb + hh * kLbTok + 4 * qd);
+                    const float4 v = *reinterpret_cast<const float4*>(lb + hh * L::LB_HEAD + 4 * qd);
                     float* dst = a.logits + static_cast<size_t>(kvh * G + g0 + hh) * a.ld + Nd + tok;
                     if (tok + 4 <= nslots) {
                         *reinterpret_cast<float4*>(dst) = v;
@@ -841,9 +849,9 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
                 vsv[i][0] = vq.x; vsv[i][1] = vq.y; vsv[i][2] = vq.z; vsv[i][3] = vq.w;
                 vzv[i][0] = zq.x; vzv[i][1] = zq.y; vzv[i][2] = zq.z; vzv[i][3] = zq.w;
             }
-            const uint2* vtr = reinterpret_cast<const uint2*>(vt_l);
-            q0 = vtr[n * (kVTS / 2) + gk];
-            q1 = vtr[(n + 16) * (kVTS / 2) + gk];
+            const int d0 = vt_dword(n, 2 * gk), d1 = vt_dword(n + 16, 2 * gk);
+            q0 = *reinterpret_cast<const uint2*>(vt_l + d0);
+            q1 = make_uint2(vt_l[d1], vt_l[d1 + 1]);
         };
         if constexpr (TP) read_v();
         if constexpr (TP) {
@@ -914,7 +922,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         if (L::LB_PAIRS > 0 && a.logits && !lo_col && chead < GP) {
 #pragma unroll
             for (int i = 0; i < NT; ++i)
-                *reinterpret_cast<float4*>(lb + chead * kLbTok + 32 * (p - pbuf) + 16 * tt(i) + 4 * gk) =
+                *reinterpret_cast<float4*>(lb + chead * L::LB_HEAD + 32 * (p - pbuf) + 16 * tt(i) + 4 * gk) =
                     make_float4(s2[i][0], s2[i][1], s2[i][2], s2[i][3]);
         }
         if (L::LB_PAIRS == 0 && a.logits && !lo_col && chead < gc) {
