@@ -9,6 +9,8 @@ a 256-token ring and 4 sinks over 2048 appends.
 """
 from __future__ import annotations
 
+import numpy as np
+
 from oracle import synth
 
 RUNS = {
@@ -59,3 +61,36 @@ def is_checkpoint(cfg: dict, s: int) -> bool:
 def engine_args(cfg: dict):
     return (cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["msl"], cfg["S"], cfg["R"], cfg["hr"], cfg["decay"], cfg["iv"],
             cfg["kgs"], cfg["fp16"])
+
+
+# Heavy-hitter argmin with tied scores (cache_engine.cpp:224-232: first slot of
+# the minimum under '<'). Tier maintenance with injected weights and no score
+# decay, so scores are sums of equal increments added in the same order and
+# many slots share the minimum.
+#  * "small": weight 1e-3 on every second dense position (sinks, heavy hitters,
+#    recent window), none on the packed store; the tier (60 slots) fills and
+#    its first minimal slot is replaced now and then;
+#  * "large": no weights for 40 steps (the first threshold is then 0, and with
+#    an update interval past the run it stays 0, so every eviction is promoted),
+#    then 1e-3 x ((s + j) % 3) on recent-window position j; the tier fills all
+#    8750 slots, beyond the 8192 scores one pass of the GPU scan covers, and
+#    positive-score evictions replace its zero-score slots in order.
+TIE_RUNS = {
+    "small": dict(args=(2, 1, 16, 1200, 4, 16, 0.05, 1.0, 16, 16), steps=1100, checkpoints=tuple(range(99, 1100, 100))),
+    "large": dict(args=(2, 1, 16, 17500, 4, 16, 0.5, 1.0, 1 << 30, 16), steps=9100, checkpoints=(8768, 8900, 9099)),
+}
+
+
+def tie_kv(s: int):
+    return synth.normal(71, 2 * s, (16,)), synth.normal(71, 2 * s + 1, (16,))
+
+
+def tie_weights(run: str, counters: dict, n: int, s: int):
+    w = np.zeros(n, np.float32)
+    ring0 = counters["s_count"] + counters["hh_count"]
+    nd = ring0 + counters["rw_count"]
+    if run == "small":
+        w[:nd:2] = 1e-3
+    elif s >= 40:
+        w[ring0:nd] = 1e-3 * ((s + np.arange(nd - ring0)) % 3)
+    return w

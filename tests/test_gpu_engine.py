@@ -211,3 +211,26 @@ def test_flush_special_values_match_oracle(C, oracle, fp16, kgs):
         if engine_runs.is_checkpoint(cfg, s):
             _compare_state(gpu_engine_state(eng), oe.state(), (fp16, kgs, s))
     assert eng.counters()["pbs_blocks_used"] >= 4
+
+
+@pytest.mark.parametrize("run,fp16", [("small", False), ("small", True), ("large", False)])
+def test_route_argmin_ties_lockstep_with_oracle(C, oracle, run, fp16):
+    """The route kernel's heavy-hitter argmin (a min over ordered 64-bit keys,
+    eight scores per thread per pass) against the oracle engine with tied scores
+    (engine_runs.TIE_RUNS): the whole state bit for bit at the checkpoints, for a
+    60-slot tier and for an 8750-slot one (more than one pass of the scan)."""
+    cfg = engine_runs.TIE_RUNS[run]
+    Hq, Hkv, D, msl, S, R, hr, decay, iv, kgs = cfg["args"]
+    eng = C.TriTierCacheEngine(Hq, Hkv, D, msl, S, R, hr, decay, iv, kgs, "fp16" if fp16 else "fp32")
+    oe = oracle.engine(*cfg["args"], fp16)
+    for s in range(cfg["steps"]):
+        k, v = engine_runs.tie_kv(s)
+        eng.ingest(dev(k), dev(v))
+        oe.ingest(k, v)
+        w = engine_runs.tie_weights(run, oe.counters(), oe.visible(), s)
+        eng.feedback(dev(w))
+        oe.feedback(w)
+        if s in cfg["checkpoints"]:
+            _compare_state(gpu_engine_state(eng), oe.state(), (run, fp16, s))
+    c = oe.counters()
+    assert c["hh_count"] == c["max_hh"]

@@ -290,3 +290,38 @@ def test_engine_buffer_bytes_matches_reference(oracle, reference, fp16, kgs, Hq,
         o.step(q, k, v)
         r.step(q, k, v)
     assert o.buffer_bytes() == r.buffer_bytes()
+
+
+# ------------------------------------------- heavy-hitter argmin with tied scores
+@pytest.mark.parametrize("run,fp16", [("small", False), ("small", True), ("large", False)])
+def test_engine_route_ties_match_reference(oracle, reference, run, fp16):
+    """Routing with tied heavy-hitter scores (engine_runs.TIE_RUNS): the oracle
+    engine's state equals the compiled reference engine's, bit for bit, through
+    the fill of the heavy-hitter tier and the replacements of its first minimal
+    slot, for a 60-slot tier and an 8750-slot one."""
+    cfg = engine_runs.TIE_RUNS[run]
+    o, r = oracle.engine(*cfg["args"], fp16), reference.engine(*cfg["args"], fp16)
+    replaced = 0
+    prev = None
+    for s in range(cfg["steps"]):
+        k, v = engine_runs.tie_kv(s)
+        o.ingest(k, v)
+        r.ingest(k, v)
+        c = o.counters()
+        if c["hh_count"] == c["max_hh"] and (s % 10 == 0 or run == "small"):
+            ids = o.buffer("HH_token_ids")[: c["hh_count"]]
+            if prev is not None and (prev != ids).any():
+                replaced += 1
+            prev = ids
+        w = engine_runs.tie_weights(run, c, o.visible(), s)
+        o.feedback(w)
+        r.feedback(w)
+        if s in cfg["checkpoints"]:
+            so, sr = o.state(), r.state()
+            assert so["counters"] == sr["counters"], s
+            for name in sr:
+                if name != "counters":
+                    assert np.array_equal(so[name].view(np.uint8), sr[name].view(np.uint8)), (s, name)
+    c = o.counters()
+    hs = o.buffer("HH_scores")[: c["hh_count"]]
+    assert c["hh_count"] == c["max_hh"] and replaced >= 3 and (hs == hs.min()).sum() > 1, (replaced, c["hh_count"])
