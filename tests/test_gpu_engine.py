@@ -234,3 +234,25 @@ def test_route_argmin_ties_lockstep_with_oracle(C, oracle, run, fp16):
             _compare_state(gpu_engine_state(eng), oe.state(), (run, fp16, s))
     c = oe.counters()
     assert c["hh_count"] == c["max_hh"]
+
+
+def test_wide_rows_route_through_eviction_buffers(C, oracle):
+    """Rows of more than 8192 floats (40 KV heads x 256) leave the ring through
+    the eviction buffers instead of registers: tier maintenance with injected
+    scores stays bit-exact with the oracle through heavy-hitter promotions, a
+    replacement in the full tier and 22 flushes."""
+    cfg = dict(mode="inject", Hq=40, Hkv=40, D=256, msl=400, S=4, R=16, hr=0.015, decay=0.999, iv=16, kgs=16,
+               fp16=False, steps=380, prefill=0, seed=31, every=95)
+    eng = gpu_engine(C, cfg)
+    oe = oracle.engine(*engine_runs.engine_args(cfg))
+    for s in range(cfg["steps"]):
+        _, K, V = engine_runs.step_inputs(cfg, s)
+        eng.ingest(dev(K), dev(V))
+        oe.ingest(K, V)
+        w = engine_runs.inject_weights(cfg, s, oe.visible())
+        eng.feedback(dev(w))
+        oe.feedback(w)
+        if engine_runs.is_checkpoint(cfg, s):
+            _compare_state(gpu_engine_state(eng), oe.state(), ("wide", s))
+    c = oe.counters()
+    assert c["pbs_blocks_used"] >= 20 and c["hh_count"] == c["max_hh"]
