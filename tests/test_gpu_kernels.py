@@ -224,6 +224,10 @@ SWEEP = [
     # two-head groups with 32-token blocks; three KV heads (the plan's uneven branch)
     (4, 2, 128, 12, 7, 32, True, "holes"),
     (12, 3, 128, 45, 11, 16, False, "tail"),
+    # groups padded inside the matrix-core workgroup: 3 of 4 heads, 5 and 6 of 8
+    (6, 2, 128, 21, 13, 16, False, "holes"),
+    (10, 2, 128, 8, 10, 16, True, "tail"),
+    (12, 2, 128, 33, 9, 32, False, "none"),
 ]
 
 
