@@ -13,7 +13,7 @@ import torch
 
 from oracle import synth
 from oracle.exact import elementwise_ratio, exact_attention, weights_rel_err
-from gpu_helpers import dev, host, make_case, quantize_blocks_gpu, rel_err, same_bits
+from gpu_helpers import attention_errors, attention_ok, dev, host, make_case, quantize_blocks_gpu, rel_err, same_bits
 
 pytestmark = pytest.mark.gpu
 
@@ -245,6 +245,40 @@ def test_fused_attention_vs_oracle(C, oracle, case):
     ids = args[10]
     if nb:
         assert np.all(mw[nd:][ids[: nb * kgs] == -1] == 0)
+
+
+def _random_shapes(n: int, seed: int):
+    """n attention shapes drawn from a fixed seed: KV heads, group size, head_dim,
+    block length, metadata width, tier lengths and the mask of the padding ids."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        Hkv = int(rng.choice([1, 2, 3, 4, 8]))
+        G = int(rng.integers(1, 10))
+        D = int(rng.choice([16, 32, 64, 128, 128, 128, 256]))
+        kgs = int(rng.choice([16, 32]))
+        nd = int(rng.choice([0, int(rng.integers(1, 40)), int(rng.integers(40, 400))]))
+        nb = int(rng.choice([0, int(rng.integers(1, 8)), int(rng.integers(8, 90))]))
+        if nd == 0 and nb == 0:
+            continue
+        mask = str(rng.choice(["none", "tail", "holes", "block"])) if nb else "none"
+        out.append((Hkv * G, Hkv, D, nd, nb, kgs, bool(rng.integers(0, 2)), mask))
+    return out
+
+
+RANDOM_SHAPES = _random_shapes(48, 20261202)
+
+
+@pytest.mark.parametrize("case", RANDOM_SHAPES, ids=[str(c) for c in RANDOM_SHAPES])
+def test_fused_attention_random_shapes_vs_oracle(C, oracle, case):
+    """48 seeded random shapes (GQA group 1-9, head_dim 16-256, ragged tiers,
+    masked ids): output and mean weights against the oracle, elementwise."""
+    Hq, Hkv, D, nd, nb, kgs, fp16, mask = case
+    args = make_case(oracle, Hq, Hkv, D, nd, nb, kgs, fp16, mask, seed=900 + RANDOM_SHAPES.index(case))
+    out, mw = _run_fused_gpu(C, args)
+    ro, rmw = oracle.fused_attention_decode(*args)
+    err = attention_errors(out, ro, mw, rmw)
+    assert attention_ok(err), (case, err)
 
 
 @pytest.mark.parametrize("qs,ks,vs,voff", [(16.0, 50.0, 1000.0, 3000.0), (0.05, 0.01, 1e-3, 0.0), (1.0, 1.0, 1e-7, 1.0)])
