@@ -228,6 +228,9 @@ SWEEP = [
     (6, 2, 128, 21, 13, 16, False, "holes"),
     (10, 2, 128, 8, 10, 16, True, "tail"),
     (12, 2, 128, 33, 9, 32, False, "none"),
+    # more than 64 query heads: the mean-weight rows of a 64-token block span 8 head groups
+    (72, 8, 64, 30, 6, 16, False, "tail"),
+    (66, 6, 128, 7, 5, 16, True, "holes"),
 ]
 
 

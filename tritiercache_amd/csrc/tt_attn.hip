@@ -478,7 +478,7 @@ __device__ __forceinline__ float wave_sum(float x) {
 // the accumulators of splits g, g + groups, ... (up to kMergeU per group and
 // block of 256 splits, all in flight together).
 constexpr int kMergeU = 16;
-__device__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
+__device__ __forceinline__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const float* ml = a.part_ml + static_cast<size_t>(h) * a.nsplit * 2;
@@ -603,6 +603,31 @@ __device__ __forceinline__ void fin_load_logits(const FinArgs& a, const int hb, 
     }
 }
 
+// The same logits for hb = 0 and u < NU without a branch: the row index is
+// clamped to Hq - 1 and the token quad to the padded row's last one, so every
+// load stays inside the logits array and is issued whatever the thread's
+// position; rows h >= Hq are never read back, and tokens i0 + e >= n are
+// masked where the values are used. Statistics loads issued before these can
+// then be waited for alone (loads return in order).
+// Eight rows (more than 4 groups of heads) keep the branches, as their
+// registers would not fit beside the statistics.
+template <int MT, int NU>
+__device__ __forceinline__ void fin_load_logits_nb(const FinArgs& a, const int hg, const int i0, const int n,
+                                                   float4 (&lgv)[8]) {
+    if constexpr (NU == 8) {
+        fin_load_logits<MT>(a, 0, hg, i0, n, lgv);
+    } else {
+        constexpr int kGroups = 256 / (MT / 4);
+        const int ic = i0 < a.ld - 4 ? i0 : a.ld - 4;  // ld: a multiple of 4, at least 4
+#pragma unroll
+        for (int u = 0; u < NU; ++u) {
+            const int h = hg + kGroups * u;
+            const int hc = h < a.Hq ? h : a.Hq - 1;
+            lgv[u] = *reinterpret_cast<const float4*>(a.logits + static_cast<size_t>(hc) * a.ld + ic);
+        }
+    }
+}
+
 // Token i's position in the score vector (-1 for none) and, for a heavy
 // hitter, its slot.
 struct FbToken {
@@ -613,9 +638,10 @@ struct FbToken {
 // Mean-weight workgroup `wg` of `nwg`: token blocks wg, wg + nwg, ... of
 // MT tokens each. The loads of a block's feedback ids and scores are
 // issued when the block starts, those of the next block's logits as soon as
-// the current ones are consumed.
-template <int MT, bool kRowstat>
-__device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, float* sh) {
+// the current ones are consumed. NU: logits rows per thread of the first head
+// round, a power of two with NU * (256 / (MT / 4)) >= min(Hq, 8 * (256 / (MT / 4))).
+template <int MT, bool kRowstat, int NU>
+__device__ __forceinline__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, float* sh) {
     constexpr int kQuads = MT / 4;         // token quads per block
     constexpr int kGroups = 256 / kQuads;  // head groups per workgroup
     const int t = threadIdx.x;
@@ -658,13 +684,17 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
     // Thread (head group hg, token quad q): heads hg, hg + kGroups, ...;
     // tokens tok0 + 4 q .. + 3. Rows are padded to a multiple of 4 floats.
     const int q = t % kQuads, hg = t / kQuads;
-    // (M_h, 1/L_h) of every head: 8 threads per head, splits j0, j0 + 8, ...
-    // (every workgroup rebuilds them: a second launch that waits for the
-    // merge costs more than these loads). Their loads are issued first: they
-    // are on the critical path, the first block's logits load (issued next)
-    // is not.
+    // (M_h, 1/L_h) of every head: 8 threads per head, splits 2 j0 + 16 u and
+    // the one after (every workgroup rebuilds them: a second launch that waits
+    // for the merge costs more than these loads). Their loads are issued
+    // first and the first block's logits loads right behind them, before the
+    // statistics are folded: both round trips overlap, and the fold waits for
+    // the statistics alone.
     float* Mh = sh;        // [Hq]
     float* iL = sh + Hq;   // [Hq]
+    float4 lgv[8];
+    constexpr int kU4 = 8;
+    bool logits_issued = false;
     if (kRowstat) {
         // published by the merge (attn_finalize_kernel's merge role)
         for (int h = t; h < Hq; h += 256) {
@@ -672,12 +702,50 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
             Mh[h] = r.x;
             iL[h] = 1.0f / (r.y > 0.0f ? r.y : 1.0f);
         }
+    } else if (NU < 8 && Hq <= 32 && a.nsplit >= 2 && a.nsplit <= 16 * kU4) {
+        // one pass, no branches around the loads: pair index j clamped to
+        // nsplit - 2 (the float4 then holds split j - 1 and j, or neither)
+        const int h = t >> 3, j0 = t & 7;
+        const int hc = h < Hq ? h : Hq - 1;
+        const float* ml = a.part_ml + static_cast<size_t>(hc) * a.nsplit * 2;
+        float4 w[kU4];
+#pragma unroll
+        for (int u = 0; u < kU4; ++u) {
+            const int j = 2 * j0 + 16 * u;
+            const int jj = j < a.nsplit - 2 ? j : a.nsplit - 2;
+            w[u] = *reinterpret_cast<const float4*>(ml + 2 * jj);
+        }
+        fin_load_logits_nb<MT, NU>(a, hg, wg * MT + 4 * q, n, lgv);
+        __builtin_amdgcn_sched_barrier(0);  // keep both sets of loads ahead of the fold
+        logits_issued = true;
+        float2 v[2 * kU4];
+#pragma unroll
+        for (int u = 0; u < kU4; ++u) {
+            const int j = 2 * j0 + 16 * u;
+            const int jj = j < a.nsplit - 2 ? j : a.nsplit - 2;
+            const float2 lo = make_float2(w[u].x, w[u].y), hi = make_float2(w[u].z, w[u].w);
+            const float2 none = make_float2(kNegInf, 0.0f);
+            v[2 * u] = (j == jj) ? lo : (j == jj + 1 ? hi : none);
+            v[2 * u + 1] = (j == jj && j + 1 < a.nsplit) ? hi : none;
+        }
+        float mx = kNegInf;
+#pragma unroll
+        for (int u = 0; u < 2 * kU4; ++u) mx = fmaxf(mx, v[u].x);
+        float ls = 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2 * kU4; ++u)
+            ls += (v[u].x == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(v[u].x - mx) * v[u].y;
+        const float gm = max8(mx);
+        const float gl = sum8((mx == kNegInf) ? 0.0f : ls * __builtin_amdgcn_exp2f(mx - gm));
+        if (j0 == 0 && h < Hq) {
+            Mh[h] = gm;
+            iL[h] = 1.0f / (gl > 0.0f ? gl : 1.0f);
+        }
     }
-    for (int h0 = 0; !kRowstat && h0 < Hq; h0 += 32) {
+    for (int h0 = 0; !kRowstat && !logits_issued && h0 < Hq; h0 += 32) {
         const int h = h0 + (t >> 3), j0 = t & 7;
         const float* ml = a.part_ml + static_cast<size_t>(h < Hq ? h : 0) * a.nsplit * 2;
         float mx = kNegInf, ls = 0.0f;
-        constexpr int kU4 = 8;
         for (int jb = 2 * j0; jb < a.nsplit; jb += 16 * kU4) {
             float2 v[2 * kU4];  // (m, l) of splits jb + 16 u and jb + 16 u + 1
 #pragma unroll
@@ -711,8 +779,7 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
             iL[h] = 1.0f / (gl > 0.0f ? gl : 1.0f);
         }
     }
-    float4 lgv[8];
-    fin_load_logits<MT>(a, 0, hg, wg * MT + 4 * q, n, lgv);
+    if (!logits_issued) fin_load_logits_nb<MT, NU>(a, hg, wg * MT + 4 * q, n, lgv);
     __syncthreads();
     float* red = sh + 2 * Hq;  // [kGroups][MT]
     for (int blk = wg; blk * MT < n; blk += nwg) {
@@ -725,7 +792,7 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
         float w4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         if (i0 < n) {
             for (int hb = 0; hb < Hq; hb += 8 * kGroups) {
-                if (hb > 0) fin_load_logits<MT>(a, hb, hg, i0, n, lgv);
+                if (hb > 0) fin_load_logits<MT>(a, hb, hg, i0, n, lgv);  // heads past 8 groups of the first round
 #pragma unroll
                 for (int u = 0; u < 8; ++u) {
                     const int h = hb + hg + kGroups * u;
@@ -735,7 +802,9 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         // s <= M_h, so 2^(s - M_h) <= 1 (flushed to 0 below 2^-126)
-                        const float w = (sc[e] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(sc[e] - mh) * il;
+                        const float w = (sc[e] == kNegInf || i0 + e >= n)
+                                            ? 0.0f
+                                            : __builtin_amdgcn_exp2f(sc[e] - mh) * il;
                         w4[e] += w;
                         if (a.head_w && i0 + e < n && i0 + e < a.head_w_ld)
                             a.head_w[static_cast<size_t>(h) * a.head_w_ld + i0 + e] = w;
@@ -744,7 +813,7 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
             }
         }
         const int nxt = blk + nwg;
-        if (nxt * MT < n) fin_load_logits<MT>(a, 0, hg, nxt * MT + 4 * q, n, lgv);
+        if (nxt * MT < n) fin_load_logits_nb<MT, NU>(a, hg, nxt * MT + 4 * q, n, lgv);
 #pragma unroll
         for (int e = 0; e < 4; ++e) red[hg * MT + 4 * q + e] = w4[e];
         __syncthreads();
@@ -765,6 +834,24 @@ __device__ void fin_mean_tokens(const FinArgs& a, const int wg, const int nwg, f
     }
 }
 
+// Logits rows per thread in the first head round of a MT-token block (see
+// fin_mean_tokens).
+template <int MT>
+__host__ __device__ constexpr int fin_rows(const int Hq) {
+    constexpr int kGroups = 256 / (MT / 4);
+    return Hq <= kGroups ? 1 : Hq <= 2 * kGroups ? 2 : Hq <= 4 * kGroups ? 4 : 8;
+}
+
+template <int MT, bool kRowstat>
+__device__ __forceinline__ void fin_mean_dispatch(const FinArgs& a, const int wg, const int nwg, float* sh) {
+    switch (fin_rows<MT>(a.Hq)) {
+    case 1: fin_mean_tokens<MT, kRowstat, 1>(a, wg, nwg, sh); break;
+    case 2: fin_mean_tokens<MT, kRowstat, 2>(a, wg, nwg, sh); break;
+    case 4: fin_mean_tokens<MT, kRowstat, 4>(a, wg, nwg, sh); break;
+    default: fin_mean_tokens<MT, kRowstat, 8>(a, wg, nwg, sh); break;
+    }
+}
+
 template <int MT>
 __global__ void __launch_bounds__(256) attn_finalize_kernel(FinArgs a) {
     extern __shared__ float sh[];
@@ -772,7 +859,7 @@ __global__ void __launch_bounds__(256) attn_finalize_kernel(FinArgs a) {
     if (b < a.Hq)
         fin_merge_head(a, b, sh);
     else
-        fin_mean_tokens<MT, false>(a, b - a.Hq, static_cast<int>(gridDim.x) - a.Hq, sh);
+        fin_mean_dispatch<MT, false>(a, b - a.Hq, static_cast<int>(gridDim.x) - a.Hq, sh);
 }
 
 // The mean-weight role alone, after a merge-only finalize of the same
@@ -780,7 +867,7 @@ __global__ void __launch_bounds__(256) attn_finalize_kernel(FinArgs a) {
 template <int MT>
 __global__ void __launch_bounds__(256) attn_mean_kernel(FinArgs a) {
     extern __shared__ float sh[];
-    fin_mean_tokens<MT, true>(a, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), sh);
+    fin_mean_dispatch<MT, true>(a, static_cast<int>(blockIdx.x), static_cast<int>(gridDim.x), sh);
 }
 
 // ---------------------------------------------------------------------------
@@ -916,7 +1003,7 @@ __global__ void __launch_bounds__(256) attn_finalize_batched_kernel(const FinBat
     const int m = blk - merges;
     const int i = batch_find(b.mean_base, b.nseq, m);
     const FinArgs a = fin_batch_args(b, i);
-    fin_mean_tokens<kMeanTokens, false>(a, m - b.mean_base[i], b.mean_base[i + 1] - b.mean_base[i], sh);
+    fin_mean_dispatch<kMeanTokens, false>(a, m - b.mean_base[i], b.mean_base[i + 1] - b.mean_base[i], sh);
 }
 
 template <int CPL, int GP>
