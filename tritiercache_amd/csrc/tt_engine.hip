@@ -310,8 +310,12 @@ __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
     const int logical = st[kLogicalAlloc], pbs_count = st[kPbsCount];
 
     // Score and threshold (cache_engine.cpp:216-218).
+    // (read without a branch around it, so that the kernel arguments it needs
+    // come in the first batch of argument loads: g holds max_seq_len >= 1 scores)
     const long long eid = a.evicted_id;
-    const float score = (eid >= 0 && eid < a.max_seq_len) ? a.g[eid] : 0.0f;
+    const bool eid_ok = eid >= 0 && eid < a.max_seq_len;
+    const float g_ev = a.g[eid_ok ? eid : 0];
+    const float score = eid_ok ? g_ev : 0.0f;
     const float thr = a.thr_zero ? 0.0f : __int_as_float(st[kThreshold]);
 
     // Evicted row out of the ring slot, new token in (each thread owns the
@@ -341,12 +345,12 @@ __global__ void __launch_bounds__(1024) route_kernel(RouteArgs a) {
     // (cache_engine.cpp:224-232): first index of the minimum under '<'; NaNs
     // never win unless at slot 0, which the decision below handles. Each
     // thread keeps kArgminBatch loads in flight, then a min over the keys.
-    // It runs whenever the heavy hitters are full, whatever the score, so
-    // that its loads go out with the others (the decision reads it only
-    // when the score passes the threshold).
-    const bool need_min = (hh >= a.max_hh) && hh > 0;
+    // The decision reads it only when the heavy hitters are full and the
+    // score passes the threshold, so it runs only then (most evicted tokens
+    // go to the waiting room without it).
+    const bool need_min = (hh >= a.max_hh) && hh > 0 && score >= thr;
     float h0 = 0.0f;  // slot 0's score, read by the decision
-    if (tid == 0 && hh >= a.max_hh) h0 = a.hh_scores[0];
+    if (tid == 0 && need_min) h0 = a.hh_scores[0];
     unsigned long long best = ~0ull;
     if (need_min) {
         for (int i0 = 0; i0 < hh; i0 += 1024 * kArgminBatch) {
