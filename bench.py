@@ -10,8 +10,15 @@ synthetic, generated on the GPU from a seed, packed by the library's own
 quantisers. Each layer has its own tier tables (1.57 GB in HBM in total), so
 every step streams from HBM, not from the 256 MB Infinity Cache.
 
-One step = for each of the 32 layers, tt_fused_attention_decode_ws (split-K
-partials, log-sum-exp merge, mean attention weights), replayed as one HIP graph.
+One step = the 32 layers one after another, each with its attention output and
+its mean attention weights, replayed as one HIP graph: per layer the split-K
+partials (tt_attention_partials) and one finalize launch that merges this
+layer's partials and computes the previous layer's mean weights
+(tt_attention_finalize_deferred, two workspaces taking turns); the last
+layer's mean weights get a launch of their own. The same step as one
+tt_fused_attention_decode_ws call per layer (merge and mean weights of a layer
+in one launch) is timed beside it (`us_per_step_per_layer_calls`), and both
+are checked to give the same outputs (bit for bit) and mean weights (1e-6).
 The dominant kernel (attn_packed_kernel: split-K partials, the packed blocks on
 the matrix cores and the FP32 tiers on the VALU) is also timed on its own: a
 HIP graph of the 32 layers' partials launches, HIP events on the launch
@@ -563,31 +570,52 @@ def main():
     tag = "16" if fp16 else "32"
     ws_bytes = int(lib.tt_fused_attention_workspace_bytes(nd, nb, Hq, Hkv, D, 16, 1))
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+    ws2 = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")  # the deferred step's other workspace
 
     def layer_args(d, t):
         return (d["Q"].data_ptr(), d["dK"].data_ptr(), d["dV"].data_ptr(), nd, d["KP"].data_ptr(),
                 d["KS" + t].data_ptr(), d["KZ" + t].data_ptr(), d["VP"].data_ptr(), d["VS" + t].data_ptr(),
                 d["VZ" + t].data_ptr(), d["ids"].data_ptr(), nb, Hq, Hkv, D)
 
-    def step(t, f16):
+    def step_per_layer(t, f16):
         for d in data:
             L.check(lib.tt_fused_attention_decode_ws(*layer_args(d, t), d["out"].data_ptr(), d["mw"].data_ptr(), 16,
                                                      f16, ws.data_ptr(), ws_bytes, sp()), "fused")
 
-    def time_steps(t, f16):
+    def step(t, f16):
+        # layer i's mean weights in layer i + 1's finalize launch, the last layer's on their own
+        wss = (ws, ws2)
+        for i, d in enumerate(data):
+            w = wss[i % 2]
+            L.check(lib.tt_attention_partials(*layer_args(d, t), 16, f16, 1, w.data_ptr(), ws_bytes, sp()),
+                    "partials")
+            if i == 0:
+                L.check(lib.tt_attention_finalize(d["Q"].data_ptr(), nd, nb, Hq, Hkv, D, d["out"].data_ptr(), None,
+                                                  16, f16, 1, w.data_ptr(), ws_bytes, sp()), "merge")
+            else:
+                L.check(lib.tt_attention_finalize_deferred(
+                    d["Q"].data_ptr(), nd, nb, Hq, Hkv, D, d["out"].data_ptr(), 16, f16, w.data_ptr(), ws_bytes,
+                    nd, nb, data[i - 1]["mw"].data_ptr(), wss[(i - 1) % 2].data_ptr(), ws_bytes, sp()), "deferred")
+        last = len(data) - 1
+        L.check(lib.tt_attention_finalize(data[last]["Q"].data_ptr(), nd, nb, Hq, Hkv, D, None,
+                                          data[last]["mw"].data_ptr(), 16, f16, 1, wss[last % 2].data_ptr(), ws_bytes,
+                                          sp()), "mean")
+
+    def time_steps(t, f16, fn=None):
+        fn = fn or step
         use_graph = not args.no_graph
         g = None
         if use_graph:
             try:
-                step(t, f16)
+                fn(t, f16)
                 torch.cuda.synchronize()
                 g = torch.cuda.CUDAGraph()
                 with torch.cuda.graph(g):
-                    step(t, f16)
+                    fn(t, f16)
             except Exception as e:  # pragma: no cover
                 print(f"[bench] graph capture failed ({e}); timing direct launches", file=sys.stderr)
                 g = None
-        run = g.replay if g is not None else (lambda: step(t, f16))
+        run = g.replay if g is not None else (lambda: fn(t, f16))
         for _ in range(args.warmup):
             run()
         torch.cuda.synchronize()
@@ -632,8 +660,18 @@ def main():
         return
 
     us_step, graphed = time_steps(tag, fp16)
+    us_step_per_layer, _ = time_steps(tag, fp16, step_per_layer)
     other_tag, other_fp16 = ("16", 1) if not fp16 else ("32", 0)
     us_step_other, _ = time_steps(other_tag, other_fp16)
+
+    # The timed step against one fused call per layer: same outputs, same mean weights.
+    step(tag, fp16)
+    torch.cuda.synchronize()
+    got = [(d["out"].clone(), d["mw"].clone()) for d in data]
+    step_per_layer(tag, fp16)
+    torch.cuda.synchronize()
+    same_out = all(torch.equal(o, d["out"]) for (o, _), d in zip(got, data))
+    mw_diff = max(float((m - d["mw"]).abs().max() / d["mw"].abs().max()) for (_, m), d in zip(got, data))
     split_us = time_split_kernel(tag, fp16, reps=max(2, min(args.steps, 10)))
     split_us_other = time_split_kernel(other_tag, other_fp16, reps=3)
 
@@ -658,7 +696,7 @@ def main():
                  h["VS" + tag], h["VZ" + tag], h["ids"], nb, Hq, Hkv, D, 16, bool(fp16))
         step(tag, fp16)
         torch.cuda.synchronize()
-        gpu_out = data[0]["out"].cpu().numpy()
+        gpu_out = data[0]["out"].cpu().numpy()  # layer 0 of the timed step
         gpu_mw = data[0]["mw"].cpu().numpy()
         phys, logical = host_cores()
         threads = int(os.environ.get("OMP_NUM_THREADS", 0) or logical) if impl.kind == "reference" else 1
@@ -726,7 +764,12 @@ def main():
                         f"{args.meta} metadata, mean attention weights computed",
             "layers": layers, "ctx": ctx, "num_q_heads": Hq, "num_kv_heads": Hkv, "head_dim": D,
             "dense_tokens": nd, "packed_tokens": npk, "blocks": nb, "meta": args.meta, "hip_graph": graphed,
+            "finalize": "per layer: partials, then one launch merging this layer and computing the previous "
+                        "layer's mean weights; the last layer's mean weights in a launch of their own",
         },
+        "us_per_step_per_layer_calls": round(us_step_per_layer, 2),
+        "per_layer_calls_match": {"outputs_bit_identical": bool(same_out),
+                                  "mean_weights_max_rel_diff": mw_diff},
         "achieved_GBps": round(step_gbps, 1),
         "pct_of_hbm_peak": round(100.0 * step_gbps / HBM_PEAK_GBPS, 2),
         "bytes_read_per_step": bpl * layers,

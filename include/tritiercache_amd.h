@@ -170,6 +170,24 @@ TT_API int tt_attention_finalize(const float* Q, int dense_count, int num_blocks
                                  float* mean_attn_weights, int k_group_size, int meta_fp16,
                                  int want_mean_weights, void* workspace, size_t workspace_bytes,
                                  void* stream);
+/* For callers that run layers back to back: the merge of this call's
+ * partials into attn_output (as tt_attention_finalize with mean_attn_weights
+ * NULL, leaving the softmax statistics in `workspace`) and, in the same launch,
+ * the mean attention weights of an earlier call that merged that way, whose
+ * partials are still in `prev_workspace` (planned with want_mean_weights = 1,
+ * prev_dense_count tokens and prev_num_blocks blocks, the same shape
+ * arguments), into prev_mean_attn_weights. The two workspaces must not
+ * overlap. A layer's mean weights then ride in the next layer's finalize
+ * launch, and only the last layer's need a launch of their own
+ * (tt_attention_finalize with attn_output NULL). No counterpart in the
+ * reference (bindings.cpp:99-178 returns both from one call). */
+TT_API int tt_attention_finalize_deferred(const float* Q, int dense_count, int num_blocks,
+                                          int num_q_heads, int num_kv_heads, int head_dim,
+                                          float* attn_output, int k_group_size, int meta_fp16,
+                                          void* workspace, size_t workspace_bytes,
+                                          int prev_dense_count, int prev_num_blocks,
+                                          float* prev_mean_attn_weights, void* prev_workspace,
+                                          size_t prev_workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Batched ragged decode: one decode step of many sequences, each with its own

@@ -256,3 +256,90 @@ def test_split_finalize_on_two_streams(lib, oracle, Hq, Hkv, D, nd, nb, kgs, fp1
     # neither output: rejected
     assert L.tt_attention_finalize(t["Q"].data_ptr(), nd, nb, Hq, Hkv, D, None, None, kgs, int(fp16), 1,
                                    ws.data_ptr(), ws_bytes, _stream()) == 1
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,kgs,fp16,sizes", [
+    (32, 8, 128, 16, False, [(300, 120), (250, 140), (330, 90)]),
+    (28, 4, 128, 16, True, [(40, 600), (70, 560), (33, 610)]),
+    (8, 2, 64, 32, False, [(40, 30), (12, 44), (64, 9)]),
+])
+def test_deferred_mean_weights_across_layers(lib, oracle, Hq, Hkv, D, kgs, fp16, sizes):
+    """Layers run back to back, each layer's mean weights computed in the next layer's finalize launch
+    (tt_attention_finalize_deferred over two alternating workspaces; the first layer merged alone, the last
+    layer's mean weights by a mean-only tt_attention_finalize) match one tt_fused_attention_decode_ws call
+    per layer: outputs bit for bit (same merge), mean weights within 1e-6 of the largest (their softmax
+    statistics come from the merge instead of being rebuilt); eagerly and as a captured graph replayed with
+    new queries. Overlapping workspaces are rejected."""
+    L = lib.load()
+    layers = []
+    for i, (nd, nb) in enumerate(sizes):
+        args = K.make_case(oracle, Hq, Hkv, D, nd, nb, kgs, fp16, "tail", seed=970 + 7 * i + Hq)
+        (Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb) = args[:12]
+        t = {k: dev(v) for k, v in dict(Q=Q, dK=dK, dV=dV, KP=KP, KS=KS, KZ=KZ, VP=VP, VS=VS, VZ=VZ, ids=ids).items()}
+        n = nd + nb * kgs
+        t.update(nd=nd, nb=nb, out=torch.empty((Hq, D), device="cuda"), mw=torch.empty((n,), device="cuda"),
+                 rout=torch.empty((Hq, D), device="cuda"), rmw=torch.empty((n,), device="cuda"))
+        layers.append(t)
+    ws_bytes = max(int(L.tt_fused_attention_workspace_bytes(t["nd"], t["nb"], Hq, Hkv, D, kgs, 1)) for t in layers)
+    ws = [torch.empty(ws_bytes, dtype=torch.uint8, device="cuda") for _ in range(2)]
+
+    def tier(t):
+        return (t["Q"].data_ptr(), t["dK"].data_ptr(), t["dV"].data_ptr(), t["nd"], t["KP"].data_ptr(),
+                t["KS"].data_ptr(), t["KZ"].data_ptr(), t["VP"].data_ptr(), t["VS"].data_ptr(), t["VZ"].data_ptr(),
+                t["ids"].data_ptr(), t["nb"], Hq, Hkv, D)
+
+    def reference():
+        for t in layers:
+            lib.check(L.tt_fused_attention_decode_ws(*tier(t), t["rout"].data_ptr(), t["rmw"].data_ptr(), kgs,
+                                                     int(fp16), ws[0].data_ptr(), ws_bytes, _stream()), "fused")
+
+    def deferred():
+        last = len(layers) - 1
+        for i, t in enumerate(layers):
+            w = ws[i % 2]
+            lib.check(L.tt_attention_partials(*tier(t), kgs, int(fp16), 1, w.data_ptr(), ws_bytes, _stream()),
+                      "partials")
+            if i == 0:
+                lib.check(L.tt_attention_finalize(t["Q"].data_ptr(), t["nd"], t["nb"], Hq, Hkv, D,
+                                                  t["out"].data_ptr(), None, kgs, int(fp16), 1, w.data_ptr(),
+                                                  ws_bytes, _stream()), "merge")
+            else:
+                p = layers[i - 1]
+                lib.check(L.tt_attention_finalize_deferred(
+                    t["Q"].data_ptr(), t["nd"], t["nb"], Hq, Hkv, D, t["out"].data_ptr(), kgs, int(fp16),
+                    w.data_ptr(), ws_bytes, p["nd"], p["nb"], p["mw"].data_ptr(), ws[(i - 1) % 2].data_ptr(),
+                    ws_bytes, _stream()), "deferred")
+        t = layers[last]
+        lib.check(L.tt_attention_finalize(t["Q"].data_ptr(), t["nd"], t["nb"], Hq, Hkv, D, None, t["mw"].data_ptr(),
+                                          kgs, int(fp16), 1, ws[last % 2].data_ptr(), ws_bytes, _stream()), "mean")
+
+    def check(tag):
+        reference()
+        torch.cuda.synchronize()
+        for i, t in enumerate(layers):
+            assert same_bits(host(t["out"]), host(t["rout"])), (tag, i)
+            r = host(t["rmw"])
+            assert np.abs(host(t["mw"]) - r).max() <= 1e-6 * np.abs(r).max(), (tag, i)
+
+    for t in layers:
+        t["out"].fill_(float("nan"))
+        t["mw"].fill_(float("nan"))
+    deferred()
+    torch.cuda.synchronize()
+    check("eager")
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        deferred()
+    for r in range(3):
+        for i, t in enumerate(layers):
+            t["Q"].copy_(dev(synth.normal(990 + 10 * r + i, 0, (Hq, D))))
+            t["out"].fill_(float("nan"))
+            t["mw"].fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        check(f"replay {r}")
+    # one workspace for both calls: rejected before any launch
+    t, p = layers[1], layers[0]
+    assert L.tt_attention_finalize_deferred(t["Q"].data_ptr(), t["nd"], t["nb"], Hq, Hkv, D, t["out"].data_ptr(), kgs,
+                                            int(fp16), ws[0].data_ptr(), ws_bytes, p["nd"], p["nb"],
+                                            p["mw"].data_ptr(), ws[0].data_ptr(), ws_bytes, _stream()) == 1

@@ -57,6 +57,8 @@ _SIGNATURES = {
     "tt_attention_partials": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
                                    _i, _vp, _sz, _vp]),
     "tt_attention_finalize": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _vp, _i, _i, _i, _vp, _sz, _vp]),
+    "tt_attention_finalize_deferred": (_i, [_vp, _i, _i, _i, _i, _i, _vp, _i, _i, _vp, _sz, _i, _i, _vp, _vp, _sz,
+                                            _vp]),
     "tt_batched_decode_workspace_bytes": (_sz, [C.POINTER(DecodeSeq), _i, _i, _i, _i, _i]),
     "tt_fused_attention_decode_batched": (_i, [C.POINTER(DecodeSeq), _vp, _i, _i, _i, _i, _i, _i, _vp, _sz, _vp]),
     "tt_engine_create": (_i, [C.POINTER(_vp), _i, _i, _i, _i, _i, _i, _f, _f, _i, _i, C.c_char_p, _vp]),

@@ -862,6 +862,20 @@ __global__ void __launch_bounds__(256) attn_finalize_kernel(FinArgs a) {
         fin_mean_dispatch<MT, false>(a, b - a.Hq, static_cast<int>(gridDim.x) - a.Hq, sh);
 }
 
+// The merge of one call's partials (workgroups [0, Hq)) beside the mean
+// weights of an earlier merge-only call whose partials, logits and row
+// statistics sit in another workspace: a caller that runs layers back to back
+// folds each layer's mean weights into the next layer's finalize launch.
+template <int MT>
+__global__ void __launch_bounds__(256) attn_finalize_deferred_kernel(FinArgs am, FinArgs aw) {
+    extern __shared__ float sh[];
+    const int b = static_cast<int>(blockIdx.x);
+    if (b < am.Hq)
+        fin_merge_head(am, b, sh);
+    else
+        fin_mean_dispatch<MT, true>(aw, b - am.Hq, static_cast<int>(gridDim.x) - am.Hq, sh);
+}
+
 // The mean-weight role alone, after a merge-only finalize of the same
 // partials: the per-head (M, L) come from the merge's row statistics.
 template <int MT>
@@ -1261,8 +1275,9 @@ int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipS
     }
 }
 
-int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out, float* mean_w,
-                         const Feedback* fb, float* head_w, int head_w_ld, hipStream_t stream, FinRoles roles) {
+namespace {
+FinArgs fin_args(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out, float* mean_w, const Feedback* fb,
+                 float* head_w, int head_w_ld) {
     char* base = static_cast<char*>(ws);
     FinArgs f;
     f.part_ml = reinterpret_cast<const float*>(base + plan.off_ml);
@@ -1282,14 +1297,34 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
     f.head_w = head_w;
     f.head_w_ld = head_w_ld;
     f.fb = fb ? *fb : Feedback{};
-    const int mt = plan.token_ub >= kMeanLongFrom ? kMeanTokensLong : kMeanTokens;
-    int mean_wgs = 0;
-    if (weights && roles != FinRoles::kMerge) {
-        const int blocks = (std::max(plan.token_ub, 1) + mt - 1) / mt;
-        const int per_wg = (blocks + kMeanMaxWgs - 1) / kMeanMaxWgs;
-        mean_wgs = (blocks + per_wg - 1) / per_wg;
-    }
-    const size_t lds = sizeof(float) * std::max<size_t>(8 + 4 * 256, 2 * static_cast<size_t>(in.Hq) + 256 * 4);
+    return f;
+}
+
+int fin_mean_tokens_per_block(const AttnPlan& plan) {
+    return plan.token_ub >= kMeanLongFrom ? kMeanTokensLong : kMeanTokens;
+}
+
+// Mean-weight workgroups of a plan (0 without weights).
+int fin_mean_wgs(const AttnPlan& plan, const bool weights) {
+    if (!weights) return 0;
+    const int mt = fin_mean_tokens_per_block(plan);
+    const int blocks = (std::max(plan.token_ub, 1) + mt - 1) / mt;
+    const int per_wg = (blocks + kMeanMaxWgs - 1) / kMeanMaxWgs;
+    return (blocks + per_wg - 1) / per_wg;
+}
+
+size_t fin_lds_bytes(const int Hq) {
+    return sizeof(float) * std::max<size_t>(8 + 4 * 256, 2 * static_cast<size_t>(Hq) + 256 * 4);
+}
+}  // namespace
+
+int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out, float* mean_w,
+                         const Feedback* fb, float* head_w, int head_w_ld, hipStream_t stream, FinRoles roles) {
+    const FinArgs f = fin_args(in, plan, ws, out, mean_w, fb, head_w, head_w_ld);
+    const bool weights = f.logits != nullptr;
+    const int mt = fin_mean_tokens_per_block(plan);
+    const int mean_wgs = fin_mean_wgs(plan, weights && roles != FinRoles::kMerge);
+    const size_t lds = fin_lds_bytes(in.Hq);
     if (roles == FinRoles::kMean) {
         if (mean_wgs == 0) return TT_OK;
         if (mt == kMeanTokensLong)
@@ -1301,6 +1336,24 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
     } else {
         hipLaunchKernelGGL(attn_finalize_kernel<kMeanTokens>, dim3(in.Hq + mean_wgs), dim3(256), lds, stream, f);
     }
+    TT_LAUNCH_CHECK();
+    return TT_OK;
+}
+
+int attn_launch_finalize_deferred(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out,
+                                  const AttnInputs& prev_in, const AttnPlan& prev_plan, void* prev_ws,
+                                  float* prev_mean_w, hipStream_t stream) {
+    const FinArgs am = fin_args(in, plan, ws, out, nullptr, nullptr, nullptr, 0);
+    const FinArgs aw = fin_args(prev_in, prev_plan, prev_ws, nullptr, prev_mean_w, nullptr, nullptr, 0);
+    if (!aw.logits) TT_FAIL(TT_ERR_RUNTIME, "deferred mean weights without logits in the earlier workspace");
+    const int mean_wgs = fin_mean_wgs(prev_plan, true);
+    const size_t lds = std::max(fin_lds_bytes(in.Hq), fin_lds_bytes(prev_in.Hq));
+    if (fin_mean_tokens_per_block(prev_plan) == kMeanTokensLong)
+        hipLaunchKernelGGL(attn_finalize_deferred_kernel<kMeanTokensLong>, dim3(in.Hq + mean_wgs), dim3(256), lds,
+                           stream, am, aw);
+    else
+        hipLaunchKernelGGL(attn_finalize_deferred_kernel<kMeanTokens>, dim3(in.Hq + mean_wgs), dim3(256), lds, stream,
+                           am, aw);
     TT_LAUNCH_CHECK();
     return TT_OK;
 }

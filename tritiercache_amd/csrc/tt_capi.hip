@@ -354,6 +354,42 @@ int tt_attention_finalize(const float* Q, int dense_count, int num_blocks, int n
                       want_mean_weights, as_stream(stream));
 }
 
+int tt_attention_finalize_deferred(const float* Q, int dense_count, int num_blocks, int num_q_heads,
+                                   int num_kv_heads, int head_dim, float* attn_output, int k_group_size,
+                                   int meta_fp16, void* workspace, size_t workspace_bytes, int prev_dense_count,
+                                   int prev_num_blocks, float* prev_mean_attn_weights, void* prev_workspace,
+                                   size_t prev_workspace_bytes, void* stream) {
+    clear_error();
+    if (!attn_output) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'attn_output' pointer address is NULL.");
+    if (!prev_mean_attn_weights)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'prev_mean_attn_weights' pointer address is NULL.");
+    if (!workspace || !prev_workspace)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "workspace or prev_workspace is NULL.");
+    const char* w0 = static_cast<const char*>(workspace);
+    const char* w1 = static_cast<const char*>(prev_workspace);
+    if (w0 < w1 + prev_workspace_bytes && w1 < w0 + workspace_bytes)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "workspace and prev_workspace overlap.");
+    // Only the workspaces are read; the tier pointers are placeholders for the
+    // shared validation.
+    AttnInputs in, prev_in;
+    AttnPlan plan, prev_plan;
+    const void* ph = workspace;
+    int rc = prepare(Q, static_cast<const float*>(ph), static_cast<const float*>(ph), dense_count,
+                     static_cast<const int32_t*>(ph), ph, ph, static_cast<const int32_t*>(ph), ph, ph,
+                     static_cast<const int64_t*>(ph), num_blocks, num_q_heads, num_kv_heads, head_dim, k_group_size,
+                     meta_fp16, true, &in, &plan);
+    if (rc) return rc;
+    rc = prepare(Q, static_cast<const float*>(ph), static_cast<const float*>(ph), prev_dense_count,
+                 static_cast<const int32_t*>(ph), ph, ph, static_cast<const int32_t*>(ph), ph, ph,
+                 static_cast<const int64_t*>(ph), prev_num_blocks, num_q_heads, num_kv_heads, head_dim, k_group_size,
+                 meta_fp16, true, &prev_in, &prev_plan);
+    if (rc) return rc;
+    if (workspace_bytes < plan.bytes || prev_workspace_bytes < prev_plan.bytes)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "workspace is NULL or smaller than tt_fused_attention_workspace_bytes().");
+    return attn_launch_finalize_deferred(in, plan, workspace, attn_output, prev_in, prev_plan, prev_workspace,
+                                         prev_mean_attn_weights, as_stream(stream));
+}
+
 size_t tt_batched_decode_workspace_bytes(const tt_decode_seq* seqs, int num_seqs, int num_q_heads, int num_kv_heads,
                                          int head_dim, int k_group_size) {
     clear_error();
