@@ -104,3 +104,33 @@ def test_batched_workspace_rejects_bad_shapes():
     assert L.tt_batched_decode_workspace_bytes(seqs, 2, 8, 2, 128, 16) == 0
     seqs[1].num_blocks = 0
     assert L.tt_batched_decode_workspace_bytes(seqs, 2, 8, 2, 128, 16) > 0
+
+
+@pytest.mark.skipif(not os.path.exists(LIB), reason="native library not built")
+def test_deferred_finalize_validates_before_launching():
+    """Host-side validation of tt_attention_finalize_deferred: every rejected call returns before any
+    kernel runs (the pointers are placeholders, never dereferenced)."""
+    from tritiercache_amd import _lib
+
+    L = _lib.load()
+    Hq, Hkv, D, kgs, nd, nb = 32, 8, 128, 16, 300, 120
+    need = int(L.tt_fused_attention_workspace_bytes(nd, nb, Hq, Hkv, D, kgs, 1))
+    assert need > 0
+    q, out, mw = 0x10000, 0x20000, 0x30000
+    ws, prev = 0x1000000, 0x1000000 + 2 * need
+
+    def call(**kw):
+        a = dict(Q=q, nd=nd, nb=nb, Hq=Hq, Hkv=Hkv, D=D, out=out, kgs=kgs, fp16=0, ws=ws, ws_bytes=need,
+                 pnd=nd, pnb=nb, pmw=mw, pws=prev, pws_bytes=need)
+        a.update(kw)
+        return L.tt_attention_finalize_deferred(a["Q"], a["nd"], a["nb"], a["Hq"], a["Hkv"], a["D"], a["out"],
+                                                a["kgs"], a["fp16"], a["ws"], a["ws_bytes"], a["pnd"], a["pnb"],
+                                                a["pmw"], a["pws"], a["pws_bytes"], None)
+
+    assert call(out=None) == 1 and "attn_output" in _lib.last_error()
+    assert call(pmw=None) == 1 and "prev_mean_attn_weights" in _lib.last_error()
+    assert call(pws=ws + need // 2) == 1 and "overlap" in _lib.last_error()
+    assert call(pws_bytes=need // 2) == 1 and "smaller" in _lib.last_error()
+    assert call(pnb=nb + 500, pws_bytes=need) == 1  # the earlier call's plan needs a larger workspace
+    assert call(Hkv=7) == 1  # query heads not a multiple of the KV heads
+    assert call(Q=None) == 1
