@@ -19,6 +19,8 @@ layer's mean weights get a launch of their own. The same step as one
 tt_fused_attention_decode_ws call per layer (merge and mean weights of a layer
 in one launch) is timed beside it (`us_per_step_per_layer_calls`), and both
 are checked to give the same outputs (bit for bit) and mean weights (1e-6).
+Steps of fewer than 16 layers (the 8-layer MHA case) report the per-layer
+calls as `value`: there the extra launch outweighs what deferring saves.
 The dominant kernel (attn_packed_kernel: split-K partials, the packed blocks on
 the matrix cores and the FP32 tiers on the VALU) is also timed on its own: a
 HIP graph of the 32 layers' partials launches, HIP events on the launch
@@ -135,6 +137,7 @@ def build_layers(torch, L, Hq, Hkv, D, ctx, layers, outliers, seed, metas=("32",
 
 
 PMC_TRAFFIC_MD = os.path.join(ROOT, "profiles", "attn_packed_kernel_llama3-8b-32k_hbm_traffic.md")
+DEFER_MIN_LAYERS = 16  # steps of at least this many layers time the deferred-mean-weights layout
 
 
 KERNEL_SOURCES = ("tt_attn.hip", "tt_attn_mfma.h", "tt_attn.h", "tt_common.h")
@@ -661,10 +664,15 @@ def main():
         pmc_driver(torch, lib, L, data, layer_args, tag, fp16, ws, ws_bytes, sp)
         return
 
-    us_step, graphed = time_steps(tag, fp16)
+    # Deferring each layer's mean weights to the next layer's finalize launch costs one extra launch per
+    # step: it pays with many layers (32: ~4%), not with few (8: ~4% slower).
+    deferred = layers >= DEFER_MIN_LAYERS
+    main_step = step if deferred else step_per_layer
+    us_step_deferred, graphed = time_steps(tag, fp16, step)
     us_step_per_layer, _ = time_steps(tag, fp16, step_per_layer)
+    us_step = us_step_deferred if deferred else us_step_per_layer
     other_tag, other_fp16 = ("16", 1) if not fp16 else ("32", 0)
-    us_step_other, _ = time_steps(other_tag, other_fp16)
+    us_step_other, _ = time_steps(other_tag, other_fp16, main_step)
 
     # The timed step against one fused call per layer: same outputs, same mean weights.
     step(tag, fp16)
@@ -696,7 +704,7 @@ def main():
              for k, v in d.items()}
         cargs = (h["Q"], h["dK"], h["dV"], nd, h["KP"].reshape(nb, 1, Hkv, D), h["KS" + tag], h["KZ" + tag], h["VP"],
                  h["VS" + tag], h["VZ" + tag], h["ids"], nb, Hq, Hkv, D, 16, bool(fp16))
-        step(tag, fp16)
+        main_step(tag, fp16)
         torch.cuda.synchronize()
         gpu_out = data[0]["out"].cpu().numpy()  # layer 0 of the timed step
         gpu_mw = data[0]["mw"].cpu().numpy()
@@ -766,10 +774,12 @@ def main():
                         f"{args.meta} metadata, mean attention weights computed",
             "layers": layers, "ctx": ctx, "num_q_heads": Hq, "num_kv_heads": Hkv, "head_dim": D,
             "dense_tokens": nd, "packed_tokens": npk, "blocks": nb, "meta": args.meta, "hip_graph": graphed,
-            "finalize": "per layer: partials, then one launch merging this layer and computing the previous "
-                        "layer's mean weights; the last layer's mean weights in a launch of their own",
+            "finalize": ("per layer: partials, then one launch merging this layer and computing the previous "
+                         "layer's mean weights; the last layer's mean weights in a launch of their own")
+            if deferred else "per layer: one fused call (partials, then merge and mean weights in one launch)",
         },
         "us_per_step_per_layer_calls": round(us_step_per_layer, 2),
+        "us_per_step_deferred_mean_weights": round(us_step_deferred, 2),
         "per_layer_calls_match": {"outputs_bit_identical": bool(same_out),
                                   "mean_weights_max_rel_diff": mw_diff},
         "achieved_GBps": round(step_gbps, 1),
