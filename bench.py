@@ -266,76 +266,106 @@ ENGINE_CONFIGS = {
 
 
 def engine_bench(args, torch, L, lib):
-    """Engine configurations: µs per decode step over all layers (eager calls, one stream)."""
+    """Engine configurations: µs per decode step over all layers (eager calls, one stream). Steps of 16 layers or
+    more also run with each layer's mean weights and score feedback in the next layer's finalize launch
+    (tt_engine_step_deferred, the last layer's flushed), on a fresh set of engines with the same data; `value` is
+    that layout's, `us_per_step_per_layer_calls` the per-layer tt_engine_step figure."""
     import numpy as np
 
     cfg = ENGINE_CONFIGS[args.config]
     Hq, Hkv, D, layers, steps = cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["layers"], cfg["steps"]
     msl = cfg.get("msl", cfg["ctx"] + steps + 64)
     sp = lambda: C.c_void_p(torch.cuda.current_stream().cuda_stream)  # noqa: E731
-    g = torch.Generator(device="cuda").manual_seed(args.seed)
-    engines = []
-    t0 = time.time()
-    for layer in range(layers):
-        h = C.c_void_p()
-        L.check(lib.tt_engine_create(C.byref(h), Hq, Hkv, D, msl, cfg["S"], cfg["R"], cfg["hr"], cfg["decay"],
-                                     cfg["iv"], cfg["kgs"], cfg["meta"].encode(), sp()), "engine_create")
-        engines.append(h)
-        if cfg["ctx"]:
-            K = torch.randn((cfg["ctx"], Hkv, D), generator=g, device="cuda")
-            V = torch.randn((cfg["ctx"], Hkv, D), generator=g, device="cuda")
-            if cfg["outliers"] == "t3":
-                for hh in range(Hkv):
-                    ch = torch.randperm(D, generator=g, device="cuda")[:4]
-                    z = torch.randn((cfg["ctx"], 4), generator=g, device="cuda")
-                    chi = (torch.randn((cfg["ctx"], 4, 3), generator=g, device="cuda") ** 2).sum(-1)
-                    K[:, hh, ch] = z / torch.sqrt(chi / 3.0)
-            L.check(lib.tt_engine_prefill(h, K.data_ptr(), V.data_ptr(), cfg["ctx"], sp()), "prefill")
-            del K, V
-    torch.cuda.synchronize()
-    print(f"[bench] {layers} engines ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
-    n_in = 8  # distinct input sets, cycled
-    Q = torch.randn((n_in, layers, Hq * D), generator=g, device="cuda")
-    Kn = torch.randn((n_in, layers, Hkv * D), generator=g, device="cuda")
-    Vn = torch.randn((n_in, layers, Hkv * D), generator=g, device="cuda")
-    out = torch.empty((layers, Hq * D), device="cuda")
-    if cfg["mode"] == "inject":
-        w = torch.softmax(2.0 * torch.randn((n_in, msl + 1024), generator=g, device="cuda"), dim=-1)
-
-    def run(s):
-        i = s % n_in
-        for layer, h in enumerate(engines):
-            if cfg["mode"] == "step":
-                L.check(lib.tt_engine_step(h, Q[i, layer].data_ptr(), Kn[i, layer].data_ptr(), Vn[i, layer].data_ptr(),
-                                           out[layer].data_ptr(), sp()), "step")
-            else:
-                L.check(lib.tt_engine_ingest(h, Kn[i, layer].data_ptr(), Vn[i, layer].data_ptr(), sp()), "ingest")
-                L.check(lib.tt_engine_feedback(h, w[i].data_ptr(), sp()), "feedback")
-
-    warm = min(args.warmup, 8)
-    for s in range(warm):
-        run(s)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for s in range(warm, steps):
-        run(s)
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1000.0 / (steps - warm)
-    cnt = np.zeros(23, np.int64)
-    L.check(lib.tt_engine_counters(engines[0], cnt.ctypes.data, sp()), "counters")
     names = lib.tt_engine_counter_names().decode().split()
-    c = dict(zip(names, (int(x) for x in cnt)))
+
+    def run_mode(deferred):
+        g = torch.Generator(device="cuda").manual_seed(args.seed)
+        engines = []
+        t0 = time.time()
+        for layer in range(layers):
+            h = C.c_void_p()
+            L.check(lib.tt_engine_create(C.byref(h), Hq, Hkv, D, msl, cfg["S"], cfg["R"], cfg["hr"], cfg["decay"],
+                                         cfg["iv"], cfg["kgs"], cfg["meta"].encode(), sp()), "engine_create")
+            engines.append(h)
+            if cfg["ctx"]:
+                K = torch.randn((cfg["ctx"], Hkv, D), generator=g, device="cuda")
+                V = torch.randn((cfg["ctx"], Hkv, D), generator=g, device="cuda")
+                if cfg["outliers"] == "t3":
+                    for hh in range(Hkv):
+                        ch = torch.randperm(D, generator=g, device="cuda")[:4]
+                        z = torch.randn((cfg["ctx"], 4), generator=g, device="cuda")
+                        chi = (torch.randn((cfg["ctx"], 4, 3), generator=g, device="cuda") ** 2).sum(-1)
+                        K[:, hh, ch] = z / torch.sqrt(chi / 3.0)
+                L.check(lib.tt_engine_prefill(h, K.data_ptr(), V.data_ptr(), cfg["ctx"], sp()), "prefill")
+                del K, V
+        torch.cuda.synchronize()
+        print(f"[bench] {layers} engines ready in {time.time() - t0:.1f}s", file=sys.stderr, flush=True)
+        n_in = 8  # distinct input sets, cycled
+        Q = torch.randn((n_in, layers, Hq * D), generator=g, device="cuda")
+        Kn = torch.randn((n_in, layers, Hkv * D), generator=g, device="cuda")
+        Vn = torch.randn((n_in, layers, Hkv * D), generator=g, device="cuda")
+        out = torch.empty((layers, Hq * D), device="cuda")
+        if cfg["mode"] == "inject":
+            w = torch.softmax(2.0 * torch.randn((n_in, msl + 1024), generator=g, device="cuda"), dim=-1)
+
+        def run(s):
+            i = s % n_in
+            for layer, h in enumerate(engines):
+                if cfg["mode"] == "step" and deferred:
+                    prev = engines[layer - 1] if layer > 0 else None
+                    L.check(lib.tt_engine_step_deferred(h, Q[i, layer].data_ptr(), Kn[i, layer].data_ptr(),
+                                                        Vn[i, layer].data_ptr(), out[layer].data_ptr(), prev, sp()),
+                            "step_deferred")
+                elif cfg["mode"] == "step":
+                    L.check(lib.tt_engine_step(h, Q[i, layer].data_ptr(), Kn[i, layer].data_ptr(),
+                                               Vn[i, layer].data_ptr(), out[layer].data_ptr(), sp()), "step")
+                else:
+                    L.check(lib.tt_engine_ingest(h, Kn[i, layer].data_ptr(), Vn[i, layer].data_ptr(), sp()), "ingest")
+                    L.check(lib.tt_engine_feedback(h, w[i].data_ptr(), sp()), "feedback")
+            if cfg["mode"] == "step" and deferred:
+                L.check(lib.tt_engine_flush_feedback(engines[-1], sp()), "flush")
+
+        warm = min(args.warmup, 8)
+        for s in range(warm):
+            run(s)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for s in range(warm, steps):
+            run(s)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1000.0 / (steps - warm)
+        cnt = np.zeros(23, np.int64)
+        L.check(lib.tt_engine_counters(engines[0], cnt.ctypes.data, sp()), "counters")
+        c = dict(zip(names, (int(x) for x in cnt)))
+        for h in engines:
+            lib.tt_engine_destroy(h)
+        torch.cuda.synchronize()
+        return us, warm, c
+
+    deferred = cfg["mode"] == "step" and layers >= DEFER_MIN_LAYERS
+    us_per_layer_calls = None
+    if deferred:
+        us, warm, c = run_mode(True)
+        us_per_layer_calls, _, c_ref = run_mode(False)
+        same_state = c == c_ref
+    else:
+        us, warm, c = run_mode(False)
     result = {
         "metric": f"engine decode step µs/step ({args.config})",
         "value": round(us, 2), "unit": "us/step", "n_gpus": 1, "steps": steps - warm, "warmup": warm,
         "ms_per_step": round(us / 1000.0, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic (seeded on the GPU)",
-        "config": {"workload": args.config, **{k: v for k, v in cfg.items()}, "max_seq_len": msl},
+        "config": {"workload": args.config, **{k: v for k, v in cfg.items()}, "max_seq_len": msl,
+                   "finalize": "mean weights and score feedback of each layer in the next layer's finalize launch"
+                   if deferred else "per layer: tt_engine_step"},
         "final_state_layer0": {k: c[k] for k in ("total_processed_tokens", "s_count", "hh_count", "rw_count",
                                                  "wr_count", "pbs_count", "pbs_blocks_used", "total_evictions")},
     }
+    if deferred:
+        result["us_per_step_per_layer_calls"] = round(us_per_layer_calls, 2)
+        result["per_layer_calls_same_counters"] = bool(same_state)
     if cfg["mode"] == "step":
         nd = c["s_count"] + c["hh_count"] + c["rw_count"]
         nb = c["pbs_blocks_used"]
@@ -344,8 +374,6 @@ def engine_bench(args, torch, L, lib):
             + nb * cfg["kgs"] * Hkv * (D // 16) * 4 + nb * cfg["kgs"] * Hkv * 2 * mb + nb * cfg["kgs"] * 8
         result["attention_bytes_per_step"] = b * layers
         result["attention_GBps"] = round(b * layers / (us * 1e-6) / 1e9, 1)
-    for h in engines:
-        lib.tt_engine_destroy(h)
     print(json.dumps(result), flush=True)
 
 

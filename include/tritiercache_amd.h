@@ -267,6 +267,22 @@ TT_API int tt_engine_step_weights(tt_engine* e, const float* Q, const float* K_n
                            int* visible_out, void* stream);
 
 /* cache_engine.cpp:271-395. K_all/V_all [q_len, Hkv, D] device f32. */
+/* tt_engine_step for callers that step the engines of a model's layers one
+ * after another: this engine's step runs up to its merged attention output,
+ * and its mean attention weights and score feedback are left pending; the
+ * pending feedback of `prev` (another engine on the same device, NULL for the
+ * first layer) runs in the same launch as this engine's merge. Each engine's
+ * pending feedback must run before its next step: it does so in the finalize
+ * launch of the next engine stepped this way, in tt_engine_flush_feedback, or
+ * at the start of any later call on that engine (step, prefill, feedback,
+ * counters, buffers) on that call's stream. The state after the feedback is
+ * the state tt_engine_step leaves (the mean weights from the merge's softmax
+ * statistics, within 1e-6 of those it rebuilds). No counterpart in the
+ * reference, whose step (cache_engine.cpp:397-541) runs its feedback last. */
+TT_API int tt_engine_step_deferred(tt_engine* e, const float* Q, const float* K_new,
+                                   const float* V_new, float* attn_output, tt_engine* prev,
+                                   void* stream);
+TT_API int tt_engine_flush_feedback(tt_engine* e, void* stream);
 TT_API int tt_engine_prefill(tt_engine* e, const float* K_all, const float* V_all, int q_len, void* stream);
 
 /* The two halves of step() around the attention, for tier maintenance in

@@ -256,3 +256,58 @@ def test_wide_rows_route_through_eviction_buffers(C, oracle):
             _compare_state(gpu_engine_state(eng), oe.state(), ("wide", s))
     c = oe.counters()
     assert c["pbs_blocks_used"] >= 20 and c["hh_count"] == c["max_hh"]
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,kgs,fp16", [(8, 2, 128, 16, False), (28, 4, 128, 16, True), (4, 1, 64, 32, False)])
+def test_deferred_feedback_chain_matches_per_layer_steps(C, Hq, Hkv, D, kgs, fp16):
+    """Three engines stepped as the layers of a model with tt_engine_step_deferred (each engine's mean weights
+    and score feedback in the next engine's finalize launch, the last engine's flushed) against three engines
+    stepped with tt_engine_step on the same inputs, through ring overflow, heavy-hitter promotion and
+    waiting-room flushes: outputs bit for bit at every step; at checkpoints the counters and tier ids equal and
+    the score vectors within 1e-5 of the largest (the deferred mean weights come from the merge's softmax
+    statistics, within 1e-6 of the rebuilt ones). Later calls on an engine with pending feedback run it first."""
+    from tritiercache_amd import _lib
+
+    L = _lib.load()
+    layers, msl, prompt, steps = 3, 720, 300, 150
+    mk = lambda: C.TriTierCacheEngine(Hq, Hkv, D, msl, 4, 64, 0.1, 0.99, 16, kgs,  # noqa: E731
+                                      "fp16" if fp16 else "fp32")
+    A = [mk() for _ in range(layers)]
+    B = [mk() for _ in range(layers)]
+    for i in range(layers):
+        K = dev(synth.normal(7000 + i, 0, (prompt, Hkv, D)))
+        V = dev(synth.normal(7100 + i, 0, (prompt, Hkv, D)))
+        A[i].prefill(K.data_ptr(), V.data_ptr(), prompt)
+        B[i].prefill(K.data_ptr(), V.data_ptr(), prompt)
+    stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    oa = torch.empty((Hq, D), device="cuda")
+    ob = torch.empty((Hq, D), device="cuda")
+
+    def check_state(tag):
+        for i in range(layers):
+            ga, gb = gpu_engine_state(A[i]), gpu_engine_state(B[i])  # reading B flushes its pending feedback
+            assert ga["counters"] == gb["counters"], (tag, i)
+            for name in ("HH_token_ids", "WR_token_ids", "PBS_token_ids", "PBS_K_Packed", "PBS_V_Packed", "HH_K", "RW_K"):
+                assert same_bits(ga[name], gb[name]), (tag, i, name)
+            sa, sb = ga["global_attn_scores"], gb["global_attn_scores"]
+            assert np.abs(sa - sb).max() <= 1e-5 * max(np.abs(sa).max(), 1e-30), (tag, i)
+
+    for s in range(steps):
+        for i in range(layers):
+            Q = dev(synth.normal(8000 + 10 * s + i, 0, (Hq, D)))
+            K = dev(synth.normal(9000 + 10 * s + i, 0, (Hkv, D)))
+            V = dev(synth.normal(9500 + 10 * s + i, 0, (Hkv, D)))
+            A[i].step(Q.data_ptr(), K.data_ptr(), V.data_ptr(), oa.data_ptr())
+            prev = B[i - 1]._h if i > 0 else None
+            _lib.check(L.tt_engine_step_deferred(B[i]._h, Q.data_ptr(), K.data_ptr(), V.data_ptr(), ob.data_ptr(),
+                                                 prev, stream()), "step_deferred")
+            assert torch.equal(oa, ob), (s, i)
+        _lib.check(L.tt_engine_flush_feedback(B[-1]._h, stream()), "flush")
+        if s % 50 == 49:
+            check_state(s)
+    c = A[0].counters()
+    assert c["total_evictions"] >= steps and c["hh_count"] > 0 and c["pbs_blocks_used"] > 0, c
+    # an engine cannot defer to itself
+    Q = dev(synth.normal(1, 0, (Hq, D)))
+    assert L.tt_engine_step_deferred(B[0]._h, Q.data_ptr(), Q.data_ptr(), Q.data_ptr(), ob.data_ptr(), B[0]._h,
+                                     stream()) == 1

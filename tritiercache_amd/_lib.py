@@ -64,6 +64,8 @@ _SIGNATURES = {
     "tt_engine_create": (_i, [C.POINTER(_vp), _i, _i, _i, _i, _i, _i, _f, _f, _i, _i, C.c_char_p, _vp]),
     "tt_engine_destroy": (_i, [_vp]),
     "tt_engine_step": (_i, [_vp, _vp, _vp, _vp, _vp, _vp]),
+    "tt_engine_step_deferred": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "tt_engine_flush_feedback": (_i, [_vp, _vp]),
     "tt_engine_step_weights": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, C.POINTER(_i), _vp]),
     "tt_engine_prefill": (_i, [_vp, _vp, _vp, _i, _vp]),
     "tt_engine_ingest": (_i, [_vp, _vp, _vp, _vp]),

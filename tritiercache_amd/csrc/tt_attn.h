@@ -86,12 +86,13 @@ enum class FinRoles { kBoth, kMerge, kMean };
 int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out, float* mean_w,
                          const Feedback* fb, float* head_w, int head_w_ld, hipStream_t stream,
                          FinRoles roles = FinRoles::kBoth);
-// One launch: the merge of (in, plan, ws) into out, and the mean weights of an
-// earlier merge-only finalize whose partials, logits and row statistics are in
-// prev_ws (planned with logits), into prev_mean_w.
+// One launch: the merge of (in, plan, ws) into out, and the mean weights (and
+// score feedback, when prev_fb is given) of an earlier merge-only finalize
+// whose partials, logits and row statistics are in prev_ws (planned with
+// logits), into prev_mean_w.
 int attn_launch_finalize_deferred(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out,
                                   const AttnInputs& prev_in, const AttnPlan& prev_plan, void* prev_ws,
-                                  float* prev_mean_w, hipStream_t stream);
+                                  float* prev_mean_w, const Feedback* prev_fb, hipStream_t stream);
 
 // Validates shapes the kernels support.
 int attn_check_shapes(int Hq, int Hkv, int D, int kgs);

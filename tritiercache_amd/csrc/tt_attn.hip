@@ -1342,9 +1342,9 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
 
 int attn_launch_finalize_deferred(const AttnInputs& in, const AttnPlan& plan, void* ws, float* out,
                                   const AttnInputs& prev_in, const AttnPlan& prev_plan, void* prev_ws,
-                                  float* prev_mean_w, hipStream_t stream) {
+                                  float* prev_mean_w, const Feedback* prev_fb, hipStream_t stream) {
     const FinArgs am = fin_args(in, plan, ws, out, nullptr, nullptr, nullptr, 0);
-    const FinArgs aw = fin_args(prev_in, prev_plan, prev_ws, nullptr, prev_mean_w, nullptr, nullptr, 0);
+    const FinArgs aw = fin_args(prev_in, prev_plan, prev_ws, nullptr, prev_mean_w, prev_fb, nullptr, 0);
     if (!aw.logits) TT_FAIL(TT_ERR_RUNTIME, "deferred mean weights without logits in the earlier workspace");
     const int mean_wgs = fin_mean_wgs(prev_plan, true);
     const size_t lds = std::max(fin_lds_bytes(in.Hq), fin_lds_bytes(prev_in.Hq));

@@ -387,7 +387,7 @@ int tt_attention_finalize_deferred(const float* Q, int dense_count, int num_bloc
     if (workspace_bytes < plan.bytes || prev_workspace_bytes < prev_plan.bytes)
         TT_FAIL(TT_ERR_INVALID_ARGUMENT, "workspace is NULL or smaller than tt_fused_attention_workspace_bytes().");
     return attn_launch_finalize_deferred(in, plan, workspace, attn_output, prev_in, prev_plan, prev_workspace,
-                                         prev_mean_attn_weights, as_stream(stream));
+                                         prev_mean_attn_weights, nullptr, as_stream(stream));
 }
 
 size_t tt_batched_decode_workspace_bytes(const tt_decode_seq* seqs, int num_seqs, int num_q_heads, int num_kv_heads,

@@ -624,6 +624,12 @@ struct tt_engine {
     float* mw = nullptr;
     size_t mw_cap = 0;
     int* host_state = nullptr;  // pinned
+    // A step whose mean weights and score feedback are still to run (its
+    // partials, logits and row statistics are in ws): tt_engine_step_deferred
+    // leaves it for the next engine's finalize launch or a flush.
+    bool fb_pending = false;
+    AttnInputs pend_in{};
+    AttnPlan pend_plan{};
 
     size_t msz() const { return fp16 ? 2 : 4; }
 };
@@ -759,7 +765,18 @@ Feedback engine_feedback_args(tt_engine* e) {
     return fb;
 }
 
+// The deferred mean weights and score feedback of e's last step, if any, on
+// stream s (before anything that reads or changes the scores or tiers).
+int engine_flush(tt_engine* e, hipStream_t s) {
+    if (!e->fb_pending) return TT_OK;
+    e->fb_pending = false;
+    const Feedback fb = engine_feedback_args(e);
+    return attn_launch_finalize(e->pend_in, e->pend_plan, e->ws, nullptr, e->mw, &fb, nullptr, 0, s, FinRoles::kMean);
+}
+
 int engine_sync_state(tt_engine* e, hipStream_t s) {
+    int rc = engine_flush(e, s);
+    if (rc) return rc;
     TT_HIP_CHECK(hipMemcpyAsync(e->host_state, e->st, kStateSlots * sizeof(int), hipMemcpyDeviceToHost, s));
     TT_HIP_CHECK(hipStreamSynchronize(s));
     return TT_OK;
@@ -874,6 +891,10 @@ int tt_engine_ingest(tt_engine* e, const float* K_new, const float* V_new, void*
     if (!K_new || !V_new) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'K_new'/'V_new' pointer address is NULL.");
     DeviceGuard dg(e->device);
     hipStream_t s = as_stream(stream);
+    {
+        const int frc = engine_flush(e, s);  // the last step's scores before this step's routing
+        if (frc) return frc;
+    }
     const int kvs = static_cast<int>(e->kvs);
     const int blocks = (kvs + 255) / 256;
     if (e->h_s < e->S) {
@@ -995,6 +1016,48 @@ int tt_engine_step(tt_engine* e, const float* Q, const float* K_new, const float
     return engine_attend(e, Q, attn_output, nullptr, 0, true, as_stream(stream));
 }
 
+int tt_engine_step_deferred(tt_engine* e, const float* Q, const float* K_new, const float* V_new, float* attn_output,
+                            tt_engine* prev, void* stream) {
+    clear_error();
+    if (!e) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "engine is NULL.");
+    if (!Q || !attn_output) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'Q'/'attn_output' pointer address is NULL.");
+    if (prev == e) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "prev must be another engine.");
+    if (prev && prev->device != e->device) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "prev lives on another device.");
+    int rc = tt_engine_ingest(e, K_new, V_new, stream);  // flushes e's own pending step first
+    if (rc) return rc;
+    DeviceGuard dg(e->device);
+    hipStream_t s = as_stream(stream);
+    rc = engine_reserve_blocks(e, e->blocks_ub, s);
+    if (rc) return rc;
+    const int dense_ub = e->h_s + e->h_routed + e->h_rw;
+    const AttnPlan p = attn_plan(dense_ub, e->blocks_ub, e->Hq, e->Hkv, e->D, e->kgs, true, e->fp16);
+    rc = engine_reserve_ws(e, p, s);
+    if (rc) return rc;
+    const AttnInputs in = engine_inputs(e, Q);
+    rc = attn_launch_split(in, p, e->ws, s);
+    if (rc) return rc;
+    if (prev && prev->fb_pending) {
+        prev->fb_pending = false;
+        const Feedback fb = engine_feedback_args(prev);
+        rc = attn_launch_finalize_deferred(in, p, e->ws, attn_output, prev->pend_in, prev->pend_plan, prev->ws,
+                                           prev->mw, &fb, s);
+    } else {
+        rc = attn_launch_finalize(in, p, e->ws, attn_output, nullptr, nullptr, nullptr, 0, s, FinRoles::kMerge);
+    }
+    if (rc) return rc;
+    e->pend_in = in;
+    e->pend_plan = p;
+    e->fb_pending = true;
+    return TT_OK;
+}
+
+int tt_engine_flush_feedback(tt_engine* e, void* stream) {
+    clear_error();
+    if (!e) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "engine is NULL.");
+    DeviceGuard dg(e->device);
+    return engine_flush(e, as_stream(stream));
+}
+
 int tt_engine_step_weights(tt_engine* e, const float* Q, const float* K_new, const float* V_new, float* attn_output,
                            float* head_weights, int head_weights_capacity, int* visible_out, void* stream) {
     clear_error();
@@ -1023,6 +1086,8 @@ int tt_engine_feedback(tt_engine* e, const float* mean_attn_weights, void* strea
     if (!mean_attn_weights) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "mean_attn_weights is NULL.");
     DeviceGuard dg(e->device);
     hipStream_t s = as_stream(stream);
+    int rc = engine_flush(e, s);
+    if (rc) return rc;
     const int n = e->S + e->max_hh + e->R + e->blocks_ub * e->chunk;
     hipLaunchKernelGGL(feedback_kernel, dim3((n + 255) / 256), dim3(256), 0, s, e->st, mean_attn_weights,
                        engine_feedback_args(e), e->kgs);
@@ -1038,6 +1103,8 @@ int tt_engine_prefill(tt_engine* e, const float* K_all, const float* V_all, int 
         TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'K_all'/'V_all' pointer address is NULL.");
     DeviceGuard dg(e->device);
     hipStream_t s = as_stream(stream);
+    int frc = engine_flush(e, s);
+    if (frc) return frc;
     const size_t kvs = e->kvs;
     PrefillArgs pa{};
     pa.st = e->st;
