@@ -270,6 +270,19 @@ struct MetaRaw<uint16_t> {
 // Even split of `count` items over `parts`: the first item of part `i`
 // (32-bit unsigned arithmetic: count * i stays below 2^32 for every
 // supported size, and a 64-bit divide is a long software loop).
+// Stores that write through the L2 (device scope): the partials and logits
+// are read by the next launch from other XCDs, and lines left dirty in the L2
+// would be written back at the end of this launch instead.
+typedef unsigned int tt_u4v __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void st_dev4(float* base, const uint32_t bytes, const uint32_t off, const float4 v) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000);
+    const tt_u4v w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, off, 0, 16 /* sc1 */);
+}
+__device__ __forceinline__ void st_dev1(float* p, const float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 __device__ __forceinline__ int part_begin(const int count, const int i, const int parts) {
     // The divide is expanded into vector instructions; readfirstlane hands the
     // (wave-uniform) result back to the scalar unit so loop bounds and the
@@ -405,7 +418,9 @@ __device__ __forceinline__ void dense_share(const SplitArgs& a, const DenseView&
                     if (gb + g < gc && cp == g) {
                         float* lr = a.logits + static_cast<size_t>(kvh * G + g0 + gb + g) * a.ld + tok0;
                         if (tok0 + 4 <= Nd) {
-                            *reinterpret_cast<float4*>(lr) = make_float4(s[0][g], s[1][g], s[2][g], s[3][g]);
+                            st_dev4(a.logits, static_cast<uint32_t>(a.in.Hq) * a.ld * 4u,
+                                    static_cast<uint32_t>((lr - a.logits) * 4),
+                                    make_float4(s[0][g], s[1][g], s[2][g], s[3][g]));
                         } else {
 #pragma unroll
                             for (int i = 0; i < 4; ++i)
@@ -513,10 +528,10 @@ __device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit,
             Ls = __builtin_fmaf(f, dg[1], Ls);
         }
         const size_t pi = static_cast<size_t>(kvh * G + g0 + g) * a.nsplit + split;
-        a.part_acc[pi * kMfD + c] = A;
+        st_dev1(a.part_acc + pi * kMfD + c, A);
         if (c == 0) {
-            a.part_ml[2 * pi] = (Ls > 0.0f) ? M : kNegInf;
-            a.part_ml[2 * pi + 1] = Ls;
+            st_dev1(a.part_ml + 2 * pi, (Ls > 0.0f) ? M : kNegInf);
+            st_dev1(a.part_ml + 2 * pi + 1, Ls);
         }
     }
 }
@@ -805,7 +820,8 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
                     const float4 v = *reinterpret_cast<const float4*>(lb + hh * L::LB_HEAD + 4 * qd);
                     float* dst = a.logits + static_cast<size_t>(kvh * G + g0 + hh) * a.ld + Nd + tok;
                     if (tok + 4 <= nslots) {
-                        *reinterpret_cast<float4*>(dst) = v;
+                        st_dev4(a.logits, static_cast<uint32_t>(a.in.Hq) * a.ld * 4u,
+                                static_cast<uint32_t>((dst - a.logits) * 4), v);
                     } else {
                         if (tok < nslots) dst[0] = v.x;
                         if (tok + 1 < nslots) dst[1] = v.y;
@@ -1109,10 +1125,10 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
             Ls = __builtin_fmaf(f, sm_l[w * GP + g], Ls);
         }
         const size_t pi = static_cast<size_t>(kvh * G + g0 + g) * a.nsplit + split;
-        a.part_acc[pi * kMfD + c] = A;
+        st_dev1(a.part_acc + pi * kMfD + c, A);
         if (c == 0) {
-            a.part_ml[2 * pi] = (Ls > 0.0f) ? M : kNegInf;
-            a.part_ml[2 * pi + 1] = Ls;
+            st_dev1(a.part_ml + 2 * pi, (Ls > 0.0f) ? M : kNegInf);
+            st_dev1(a.part_ml + 2 * pi + 1, Ls);
         }
     }
 }
