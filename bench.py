@@ -782,7 +782,7 @@ def main():
 
     traffic, traffic_stale = traffic_from_profile(args.config, args.meta)
     result = {
-        "metric": METRIC,
+        "metric": METRIC if args.config == "llama3-8b-32k" else f"decode-attn µs/step + achieved HBM GB/s ({args.config})",
         "value": round(us_step, 2),
         "unit": "us/step",
         "n_gpus": 1,
