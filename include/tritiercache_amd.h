@@ -275,7 +275,10 @@ TT_API int tt_engine_step_weights(tt_engine* e, const float* Q, const float* K_n
  * pending feedback must run before its next step: it does so in the finalize
  * launch of the next engine stepped this way, in tt_engine_flush_feedback, or
  * at the start of any later call on that engine (step, prefill, feedback,
- * counters, buffers) on that call's stream. The state after the feedback is
+ * counters, buffers) on that call's stream, which must be ordered after the
+ * stream of the step that left it (the same stream, or the caller's events).
+ * A call that fails to launch the pending feedback leaves it pending. The
+ * state after the feedback is
  * the state tt_engine_step leaves (the mean weights from the merge's softmax
  * statistics, within 1e-6 of those it rebuilds). No counterpart in the
  * reference, whose step (cache_engine.cpp:397-541) runs its feedback last. */

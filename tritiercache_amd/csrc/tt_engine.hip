@@ -769,9 +769,11 @@ Feedback engine_feedback_args(tt_engine* e) {
 // stream s (before anything that reads or changes the scores or tiers).
 int engine_flush(tt_engine* e, hipStream_t s) {
     if (!e->fb_pending) return TT_OK;
-    e->fb_pending = false;
     const Feedback fb = engine_feedback_args(e);
-    return attn_launch_finalize(e->pend_in, e->pend_plan, e->ws, nullptr, e->mw, &fb, nullptr, 0, s, FinRoles::kMean);
+    const int rc =
+        attn_launch_finalize(e->pend_in, e->pend_plan, e->ws, nullptr, e->mw, &fb, nullptr, 0, s, FinRoles::kMean);
+    if (rc == TT_OK) e->fb_pending = false;
+    return rc;
 }
 
 int engine_sync_state(tt_engine* e, hipStream_t s) {
@@ -1037,10 +1039,10 @@ int tt_engine_step_deferred(tt_engine* e, const float* Q, const float* K_new, co
     rc = attn_launch_split(in, p, e->ws, s);
     if (rc) return rc;
     if (prev && prev->fb_pending) {
-        prev->fb_pending = false;
         const Feedback fb = engine_feedback_args(prev);
         rc = attn_launch_finalize_deferred(in, p, e->ws, attn_output, prev->pend_in, prev->pend_plan, prev->ws,
                                            prev->mw, &fb, s);
+        if (rc == TT_OK) prev->fb_pending = false;
     } else {
         rc = attn_launch_finalize(in, p, e->ws, attn_output, nullptr, nullptr, nullptr, 0, s, FinRoles::kMerge);
     }
