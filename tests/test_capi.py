@@ -134,3 +134,36 @@ def test_deferred_finalize_validates_before_launching():
     assert call(pnb=nb + 500, pws_bytes=need) == 1  # the earlier call's plan needs a larger workspace
     assert call(Hkv=7) == 1  # query heads not a multiple of the KV heads
     assert call(Q=None) == 1
+
+
+def test_logits_larger_than_4gib_are_rejected():
+    """The kernels store the logits of the mean weights through buffer resources (a 32-bit byte range):
+    calls whose logits would pass 4 GiB fail on the host, for one sequence, a batch and an engine."""
+    import ctypes as C
+    from tritiercache_amd import _lib
+
+    L = _lib.load()
+    Hq, Hkv, D, kgs = 64, 8, 128, 16
+    nd_big = (1 << 32) // (4 * Hq) + 16  # one row of Hq logits past 4 GiB
+    p = 0x10000
+    rc = L.tt_attention_partials(p, p, p, nd_big, p, p, p, p, p, p, p, 0, Hq, Hkv, D, kgs, 0, 1, p, 1 << 62, None)
+    assert rc == 1 and "4 GiB" in _lib.last_error()
+    # without mean weights there are no logits, and the same call passes validation (its workspace is too small)
+    rc = L.tt_attention_partials(p, p, p, nd_big, p, p, p, p, p, p, p, 0, Hq, Hkv, D, kgs, 0, 0, p, 256, None)
+    assert rc == 1 and "4 GiB" not in _lib.last_error()
+
+    seqs = (_lib.DecodeSeq * 2)()
+    for i, (nd, mw) in enumerate([(300, p), (nd_big, p)]):
+        s = seqs[i]
+        s.Q, s.dense_K, s.dense_V = p, p, p
+        s.PBS_K_Packed = s.PBS_K_Scales = s.PBS_K_Zeroes = s.PBS_V_Packed = s.PBS_V_Scales = s.PBS_V_Zeroes = p
+        s.PBS_token_ids, s.attn_output, s.mean_attn_weights = p, p, mw
+        s.dense_count, s.num_blocks = nd, 4
+    assert L.tt_batched_decode_workspace_bytes(seqs, 2, Hq, Hkv, D, kgs) == 0
+    assert "4 GiB" in _lib.last_error()
+    seqs[1].mean_attn_weights = None
+    assert L.tt_batched_decode_workspace_bytes(seqs, 2, Hq, Hkv, D, kgs) > 0
+
+    eng = C.c_void_p()
+    rc = L.tt_engine_create(C.byref(eng), Hq, Hkv, D, nd_big, 4, 256, 0.05, 0.999, 32, kgs, b"fp32", None)
+    assert rc == 1 and "4 GiB" in _lib.last_error() and not eng.value

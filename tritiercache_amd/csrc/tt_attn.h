@@ -100,6 +100,10 @@ int attn_check_shapes(int Hq, int Hkv, int D, int kgs);
 // Whether head_dim D runs on the matrix-core split kernel (and the batched one).
 bool use_packed_kernel(int D);
 
+// Whether a logits buffer of Hq rows of ld floats stays within 4 GiB: the
+// kernels store it through buffer resources, whose byte range is 32-bit.
+inline bool logits_fit(long long Hq, long long ld) { return Hq * ld * 4LL <= 0xFFFFFFFFLL; }
+
 // Batched ragged decode (head_dim 128): sequences per launch; their plan
 // travels in the kernel arguments.
 constexpr int kMaxBatchSeqs = 64;

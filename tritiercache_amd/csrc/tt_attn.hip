@@ -1243,6 +1243,8 @@ AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs,
 }
 
 int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipStream_t stream) {
+    if (plan.logits && !logits_fit(in.Hq, plan.ld))
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_q_heads x tokens exceeds the 4 GiB logits buffer of the mean weights.");
     char* base = static_cast<char*>(ws);
     SplitArgs a;
     a.in = in;

@@ -94,6 +94,8 @@ int prepare(const float* Q, const float* dK, const float* dV, int dense_count, c
     if (num_blocks > 0 && (!KP || !KS || !KZ || !VP || !VS || !VZ || !ids))
         TT_FAIL(TT_ERR_INVALID_ARGUMENT, "PBS arguments must be non-NULL when num_blocks > 0.");
     *plan = attn_plan(dense_count, num_blocks, Hq, Hkv, D, kgs, want_mw, meta_fp16);
+    if (want_mw && !logits_fit(Hq, plan->ld))
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_q_heads x tokens exceeds the 4 GiB logits buffer of the mean weights.");
     in->Q = Q;
     in->k0 = dK;
     in->v0 = dV;
@@ -156,6 +158,9 @@ int check_batch(const tt_decode_seq* seqs, int num_seqs, int Hq, int Hkv, int D,
         const tt_decode_seq& q = seqs[i];
         tokens += static_cast<long long>(q.dense_count) + static_cast<long long>(q.num_blocks) * kgs + 4;
         if (tokens > INT_MAX) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "the batch holds more than 2^31 tokens.");
+        const long long tub = static_cast<long long>(q.dense_count) + static_cast<long long>(q.num_blocks) * kgs;
+        if (q.mean_attn_weights && !logits_fit(Hq, (tub + 3) & ~3LL))
+            TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_q_heads x tokens exceeds the 4 GiB logits buffer of the mean weights.");
         AttnInputs in;
         AttnPlan plan;
         rc = prepare(q.Q, q.dense_K, q.dense_V, q.dense_count, q.PBS_K_Packed, q.PBS_K_Scales, q.PBS_K_Zeroes,

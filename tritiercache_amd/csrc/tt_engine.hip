@@ -812,6 +812,15 @@ int tt_engine_create(tt_engine** out, int num_q_heads, int num_kv_heads, int hea
     if (max_seq_len <= 0) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "max_seq_len must be positive.");
     if (sink_size < 0 || rw_size < 1)
         TT_FAIL(TT_ERR_INVALID_ARGUMENT, "sink_size must be >= 0 and rw_size must be >= 1.");
+    {
+        // the attention's tokens at most: sinks, heavy hitters, ring, every block
+        const long long hh = std::max(1LL, static_cast<long long>(std::ceil(static_cast<float>(max_seq_len) * h_ratio)));
+        const long long tokens = static_cast<long long>(sink_size) + hh + rw_size +
+                                 (static_cast<long long>(max_seq_len) / kgs + 2) * kgs;
+        if (!logits_fit(num_q_heads, (tokens + 3) & ~3LL))
+            TT_FAIL(TT_ERR_INVALID_ARGUMENT,
+                    "num_q_heads x max_seq_len exceeds the 4 GiB logits buffer of the mean weights.");
+    }
     hipStream_t s = as_stream(stream);
     tt_engine* e = new tt_engine();
     TT_HIP_CHECK(hipGetDevice(&e->device));
