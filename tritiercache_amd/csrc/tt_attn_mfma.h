@@ -277,9 +277,6 @@ struct MetaRaw<uint16_t> {
     __device__ __forceinline__ static float f1(const One v) { return f16_to_f32(static_cast<uint16_t>(v)); }
 };
 
-// Even split of `count` items over `parts`: the first item of part `i`
-// (32-bit unsigned arithmetic: count * i stays below 2^32 for every
-// supported size, and a 64-bit divide is a long software loop).
 // Stores that write through the L2 (device scope): the partials and logits
 // are read by the next launch from other XCDs, and lines left dirty in the L2
 // would be written back at the end of this launch instead.
@@ -293,12 +290,18 @@ __device__ __forceinline__ void st_dev1(float* p, const float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Even split of `count` items over `parts`: the first item of part `i`,
+// floor(count * i / parts), in 32-bit arithmetic for any count < 2^31 and
+// i <= parts < 2^16 (a 64-bit divide is a long software loop):
+// count * i = (q * parts + r) * i, so the floor is q * i + floor(r * i / parts)
+// with r * i < parts^2.
 __device__ __forceinline__ int part_begin(const int count, const int i, const int parts) {
-    // The divide is expanded into vector instructions; readfirstlane hands the
-    // (wave-uniform) result back to the scalar unit so loop bounds and the
+    // The divides are expanded into vector instructions; readfirstlane hands
+    // the (wave-uniform) result back to the scalar unit so loop bounds and the
     // branches that depend on them stay uniform.
-    return __builtin_amdgcn_readfirstlane(
-        static_cast<int>(static_cast<unsigned>(count) * static_cast<unsigned>(i) / static_cast<unsigned>(parts)));
+    const unsigned c = static_cast<unsigned>(count), n = static_cast<unsigned>(parts), k = static_cast<unsigned>(i);
+    const unsigned q = c / n, r = c - q * n;
+    return __builtin_amdgcn_readfirstlane(static_cast<int>(q * k + r * k / n));
 }
 
 // FP32 16-token tiles [d0, d1) of FP32 workgroup `dsplit` of nsplit_d.
@@ -363,7 +366,7 @@ __device__ __forceinline__ void dense_load(const AttnInputs& in, const DenseView
         const int idx = in0 ? r : (in1 ? r - dv.n0 : ring);
         const float* kb = in0 ? in.k0 : (in1 ? in.k1 : in.k2);
         const float* vb = in0 ? in.v0 : (in1 ? in.v1 : in.v2);
-        const int off = (idx * in.Hkv + kvh) * kMfD + cp * 8;
+        const size_t off = (static_cast<size_t>(idx) * in.Hkv + kvh) * kMfD + cp * 8;
         load_f32<8>(kb + off, t.kx[i]);
         load_f32<8>(vb + off, t.vx[i]);
     }
