@@ -359,7 +359,8 @@ def engine_bench(args, torch, L, lib):
         "dtype": "f32", "data": "synthetic (seeded on the GPU)",
         "config": {"workload": args.config, **{k: v for k, v in cfg.items()}, "max_seq_len": msl,
                    "finalize": "mean weights and score feedback of each layer in the next layer's finalize launch"
-                   if deferred else "per layer: tt_engine_step"},
+                   if deferred else ("per layer: tt_engine_step" if cfg["mode"] == "step" else
+                                     "per layer: tt_engine_ingest, then tt_engine_feedback with injected weights")},
         "final_state_layer0": {k: c[k] for k in ("total_processed_tokens", "s_count", "hh_count", "rw_count",
                                                  "wr_count", "pbs_count", "pbs_blocks_used", "total_evictions")},
     }
