@@ -107,7 +107,9 @@ TT_API int tt_fused_attention_decode(const float* Q, const float* dense_K, const
                               int meta_fp16, void* stream);
 
 /* Same computation with a caller-provided device workspace of at least
- * tt_fused_attention_workspace_bytes(...) bytes. No allocation. */
+ * tt_fused_attention_workspace_bytes(...) bytes. No allocation. The size
+ * query validates its arguments as the entry points do and returns 0 (with
+ * tt_last_error set) for arguments they would reject. */
 TT_API size_t tt_fused_attention_workspace_bytes(int dense_count, int num_blocks, int num_q_heads,
                                           int num_kv_heads, int head_dim, int k_group_size,
                                           int want_mean_weights);

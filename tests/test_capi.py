@@ -167,3 +167,24 @@ def test_logits_larger_than_4gib_are_rejected():
     eng = C.c_void_p()
     rc = L.tt_engine_create(C.byref(eng), Hq, Hkv, D, nd_big, 4, 256, 0.05, 0.999, 32, kgs, b"fp32", None)
     assert rc == 1 and "4 GiB" in _lib.last_error() and not eng.value
+
+
+def test_workspace_size_query_validates_like_the_entry_points():
+    """tt_fused_attention_workspace_bytes returns 0 and sets the error for arguments the attention entry
+    points reject, including token counts past int and logits past 4 GiB, and a size otherwise."""
+    from tritiercache_amd import _lib
+
+    L = _lib.load()
+    q = L.tt_fused_attention_workspace_bytes
+    for args, msg in [((-1, 5, 32, 8, 128, 16, 1), "dense_count"), ((10, -2, 32, 8, 128, 16, 1), "num_blocks"),
+                      ((10, 5, 32, 7, 128, 16, 1), "multiple"), ((10, 5, 32, 8, 96, 16, 1), "head_dim"),
+                      ((10, 5, 32, 8, 128, 24, 1), "k_group_size"),
+                      ((1 << 30, 1 << 26, 64, 8, 128, 32, 1), "2^31"),
+                      ((1 << 28, 0, 64, 8, 128, 16, 1), "4 GiB")]:
+        assert q(*args) == 0 and msg in _lib.last_error(), (args, _lib.last_error())
+    assert q(1 << 28, 0, 64, 8, 128, 16, 0) > 0  # no mean weights: no logits
+    assert q(300, 120, 32, 8, 128, 16, 1) > 0 and _lib.last_error() == ""
+    # the entry points reject the same token count
+    p = 0x10000
+    rc = L.tt_attention_partials(p, p, p, 1 << 30, p, p, p, p, p, p, p, 1 << 26, 64, 8, 128, 32, 0, 0, p, 1 << 40, None)
+    assert rc == 1 and "2^31" in _lib.last_error()

@@ -79,7 +79,12 @@ int scratch_address(void** out) {
 int check_common(int dense_count, int num_blocks, int Hq, int Hkv, int D, int kgs) {
     if (dense_count < 0) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "dense_count must be non-negative.");
     if (num_blocks < 0) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_blocks must be non-negative.");
-    return attn_check_shapes(Hq, Hkv, D, kgs);
+    const int rc = attn_check_shapes(Hq, Hkv, D, kgs);
+    if (rc) return rc;
+    // token positions and the padded logits rows are int
+    if (static_cast<long long>(dense_count) + static_cast<long long>(num_blocks) * kgs > INT_MAX - 64)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "dense_count + num_blocks x k_group_size must stay below 2^31.");
+    return TT_OK;
 }
 
 // Validates the stateless attention arguments and fills the kernel inputs and plan.
@@ -309,13 +314,19 @@ int tt_fused_attention_decode_noalloc(const float* Q, const float* dense_K, cons
 
 size_t tt_fused_attention_workspace_bytes(int dense_count, int num_blocks, int num_q_heads, int num_kv_heads,
                                           int head_dim, int k_group_size, int want_mean_weights) {
-    if (dense_count < 0 || num_blocks < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
+    clear_error();
+    if (check_common(dense_count, num_blocks, num_q_heads, num_kv_heads, head_dim, k_group_size) != TT_OK) return 0;
     // The largest plan over both metadata types (their split counts can differ).
     size_t b = 0;
-    for (int f = 0; f < 2; ++f)
-        b = std::max(b, attn_plan(dense_count, num_blocks, num_q_heads, num_kv_heads, head_dim, k_group_size,
-                                  want_mean_weights != 0, f)
-                            .bytes);
+    for (int f = 0; f < 2; ++f) {
+        const AttnPlan p = attn_plan(dense_count, num_blocks, num_q_heads, num_kv_heads, head_dim, k_group_size,
+                                     want_mean_weights != 0, f);
+        if (want_mean_weights && !logits_fit(num_q_heads, p.ld)) {
+            set_error("num_q_heads x tokens exceeds the 4 GiB logits buffer of the mean weights.");
+            return 0;
+        }
+        b = std::max(b, p.bytes);
+    }
     return b;
 }
 
