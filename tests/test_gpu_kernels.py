@@ -145,6 +145,35 @@ def test_quantize_v_unaligned_rows_vs_oracle(C, oracle, fp16):
 
 
 @pytest.mark.parametrize("fp16", [False, True])
+def test_k_block_calls_past_the_grid_y_extent(C, oracle, fp16):
+    """One quantize_k / dequantize_k call over more blocks than a grid's y extent (65535): the launches
+    are sliced, and the blocks on both sides of the seam, the first and the last match the oracle."""
+    import ctypes as ct
+    from tritiercache_amd import _lib
+
+    L = _lib.load()
+    H, D, kgs, nb = 1, 16, 16, 65535 + 21
+    mdt, _ = _meta(fp16)
+    K = torch.randn((nb * kgs, H, D), generator=torch.Generator(device="cuda").manual_seed(77), device="cuda")
+    p = torch.zeros((nb, H, D), dtype=torch.int32, device="cuda")
+    sc = torch.zeros((nb, H, D), dtype=mdt, device="cuda")
+    z = torch.zeros((nb, H, D), dtype=mdt, device="cuda")
+    sp = ct.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(L.tt_quantize_k_block(K.data_ptr(), p.data_ptr(), sc.data_ptr(), z.data_ptr(), nb, H, D, kgs,
+                                     int(fp16), sp))
+    out = torch.zeros((nb * kgs, H, D), dtype=torch.float32, device="cuda")
+    _lib.check(L.tt_dequantize_k(p.data_ptr(), sc.data_ptr(), z.data_ptr(), out.data_ptr(), nb, H, D, kgs,
+                                 int(fp16), sp))
+    torch.cuda.synchronize()
+    hk, hp, hs, hz, ho = host(K), host(p), host(sc), host(z), host(out)
+    for b in (0, 1, 65533, 65534, 65535, 65536, nb - 1):
+        op, os_, oz = oracle.quantize_k(hk[b * kgs:(b + 1) * kgs], kgs, fp16)
+        assert same_bits(hp[b], op[0]) and same_bits(hs[b], os_) and same_bits(hz[b], oz), b
+        od = oracle.dequantize_k(op, os_[None], oz[None], 1, H, D, kgs, fp16)
+        assert same_bits(ho[b * kgs:(b + 1) * kgs], od), b
+
+
+@pytest.mark.parametrize("fp16", [False, True])
 def test_dequantize_vs_oracle(C, oracle, fp16):
     H, D, nb, kgs = 4, 64, 5, 32
     K = synth.normal(31, 0, (nb * kgs, H, D))

@@ -14,18 +14,23 @@ namespace tt {
 
 namespace {
 
+constexpr int kMaxGridY = 65535;  // largest grid y extent
+// threads of a 1-D launch at most (a dispatch counts its work-items in 32 bits)
+constexpr long long kMaxThreads = 0xFFFFFF00LL;
+
 // One thread per (block, head, channel). Channels below 8*floor(D/8) follow
 // the 8-wide vector body of the reference (MINPS/MAXPS operand order), the
-// rest follow its scalar tail (std::min/std::max). The output block is
-// blockIdx.y + *base_dev when base_dev is given (engine prefill).
+// rest follow its scalar tail (std::min/std::max). Block b = b_off +
+// blockIdx.y of the input; the output block is b + *base_dev when base_dev is
+// given (engine prefill).
 template <typename MetaT>
 __global__ void __launch_bounds__(256) quantize_k_kernel(const float* __restrict__ K, uint32_t* __restrict__ packed,
                                                          MetaT* __restrict__ scale, MetaT* __restrict__ zero, int H,
-                                                         int D, int kgs, const int* __restrict__ base_dev) {
+                                                         int D, int kgs, const int* __restrict__ base_dev, int b_off) {
     const int row = H * D;
     const int hc = blockIdx.x * blockDim.x + threadIdx.x;
     if (hc >= row) return;
-    const int b = blockIdx.y;
+    const int b = b_off + static_cast<int>(blockIdx.y);
     const int ob = b + (base_dev ? *base_dev : 0);
     const int c = hc % D;
     const size_t mi = static_cast<size_t>(ob) * row + hc;
@@ -72,11 +77,11 @@ template <typename MetaT>
 __global__ void __launch_bounds__(256) dequantize_k_kernel(const int32_t* __restrict__ packed,
                                                            const MetaT* __restrict__ scale,
                                                            const MetaT* __restrict__ zero, float* __restrict__ out,
-                                                           int H, int D, int kgs) {
+                                                           int H, int D, int kgs, int b_off) {
     const int row = H * D;
     const int hc = blockIdx.x * blockDim.x + threadIdx.x;
     if (hc >= row) return;
-    const int b = blockIdx.y;
+    const int b = b_off + static_cast<int>(blockIdx.y);
     const float s = Meta<MetaT>::load(scale, static_cast<size_t>(b) * row + hc);
     const float z = Meta<MetaT>::load(zero, static_cast<size_t>(b) * row + hc);
     const int words = kgs / 16;
@@ -113,14 +118,17 @@ __global__ void __launch_bounds__(256) dequantize_v_kernel(const int32_t* __rest
 int launch_quantize_k(const float* K, uint32_t* packed, void* scale, void* zero, int num_blocks, int H, int D,
                       int kgs, int meta_fp16, const int* base_dev, hipStream_t stream) {
     if (num_blocks <= 0 || H * D <= 0) return TT_OK;
-    const dim3 grid((H * D + 255) / 256, num_blocks);
-    if (meta_fp16)
-        hipLaunchKernelGGL(quantize_k_kernel<uint16_t>, grid, dim3(256), 0, stream, K, packed,
-                           static_cast<uint16_t*>(scale), static_cast<uint16_t*>(zero), H, D, kgs, base_dev);
-    else
-        hipLaunchKernelGGL(quantize_k_kernel<float>, grid, dim3(256), 0, stream, K, packed, static_cast<float*>(scale),
-                           static_cast<float*>(zero), H, D, kgs, base_dev);
-    TT_LAUNCH_CHECK();
+    // blocks in slices of at most kMaxGridY (the grid's y extent)
+    for (int b0 = 0; b0 < num_blocks; b0 += kMaxGridY) {
+        const dim3 grid((H * D + 255) / 256, std::min(kMaxGridY, num_blocks - b0));
+        if (meta_fp16)
+            hipLaunchKernelGGL(quantize_k_kernel<uint16_t>, grid, dim3(256), 0, stream, K, packed,
+                               static_cast<uint16_t*>(scale), static_cast<uint16_t*>(zero), H, D, kgs, base_dev, b0);
+        else
+            hipLaunchKernelGGL(quantize_k_kernel<float>, grid, dim3(256), 0, stream, K, packed,
+                               static_cast<float*>(scale), static_cast<float*>(zero), H, D, kgs, base_dev, b0);
+        TT_LAUNCH_CHECK();
+    }
     return TT_OK;
 }
 
@@ -131,6 +139,7 @@ int launch_quantize_v(const float* V, int32_t* packed, void* scale, void* zero, 
     if (group == 0) {
         if (base_dev) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "quantize_v: head_dim above 1024 in the engine");
         const long long rows = static_cast<long long>(tokens) * H;
+        if (rows > kMaxThreads) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "quantize_v: tokens x heads too large for one call");
         const dim3 grid(static_cast<unsigned>((rows + 255) / 256));
         if (meta_fp16)
             hipLaunchKernelGGL(quantize_v_serial_kernel<uint16_t>, grid, dim3(256), 0, stream, V, packed,
@@ -142,6 +151,7 @@ int launch_quantize_v(const float* V, int32_t* packed, void* scale, void* zero, 
         return TT_OK;
     }
     const long long n = static_cast<long long>(tokens) * H * group;
+    if (n > kMaxThreads) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "quantize_v: tokens x heads too large for one call");
     const dim3 grid(static_cast<unsigned>((n + 255) / 256));
     if (meta_fp16)
         hipLaunchKernelGGL(quantize_v_kernel<uint16_t>, grid, dim3(256), 0, stream, V, packed,
@@ -157,14 +167,17 @@ int launch_quantize_v(const float* V, int32_t* packed, void* scale, void* zero, 
 int launch_dequantize_k(const int32_t* packed, const void* scale, const void* zero, float* out, int num_blocks,
                         int H, int D, int kgs, int meta_fp16, hipStream_t stream) {
     if (num_blocks <= 0 || H * D <= 0) return TT_OK;
-    const dim3 grid((H * D + 255) / 256, num_blocks);
-    if (meta_fp16)
-        hipLaunchKernelGGL(dequantize_k_kernel<uint16_t>, grid, dim3(256), 0, stream, packed,
-                           static_cast<const uint16_t*>(scale), static_cast<const uint16_t*>(zero), out, H, D, kgs);
-    else
-        hipLaunchKernelGGL(dequantize_k_kernel<float>, grid, dim3(256), 0, stream, packed,
-                           static_cast<const float*>(scale), static_cast<const float*>(zero), out, H, D, kgs);
-    TT_LAUNCH_CHECK();
+    for (int b0 = 0; b0 < num_blocks; b0 += kMaxGridY) {
+        const dim3 grid((H * D + 255) / 256, std::min(kMaxGridY, num_blocks - b0));
+        if (meta_fp16)
+            hipLaunchKernelGGL(dequantize_k_kernel<uint16_t>, grid, dim3(256), 0, stream, packed,
+                               static_cast<const uint16_t*>(scale), static_cast<const uint16_t*>(zero), out, H, D,
+                               kgs, b0);
+        else
+            hipLaunchKernelGGL(dequantize_k_kernel<float>, grid, dim3(256), 0, stream, packed,
+                               static_cast<const float*>(scale), static_cast<const float*>(zero), out, H, D, kgs, b0);
+        TT_LAUNCH_CHECK();
+    }
     return TT_OK;
 }
 
@@ -172,6 +185,7 @@ int launch_dequantize_v(const int32_t* packed, const void* scale, const void* ze
                         int D, int meta_fp16, hipStream_t stream) {
     const long long n = static_cast<long long>(tokens) * H * (D / 16);
     if (n <= 0) return TT_OK;
+    if (n > kMaxThreads) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "dequantize_v: tokens x heads too large for one call");
     const dim3 grid(static_cast<unsigned>((n + 255) / 256));
     if (meta_fp16)
         hipLaunchKernelGGL(dequantize_v_kernel<uint16_t>, grid, dim3(256), 0, stream, packed,
