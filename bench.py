@@ -357,7 +357,7 @@ def engine_bench(args, torch, L, lib):
         "value": round(us, 2), "unit": "us/step", "n_gpus": 1, "steps": steps - warm, "warmup": warm,
         "ms_per_step": round(us / 1000.0, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "f32", "data": "synthetic (seeded on the GPU)",
-        "config": {"workload": args.config, **{k: v for k, v in cfg.items()}, "max_seq_len": msl,
+        "config": {"workload": args.config, **{k: v for k, v in cfg.items()}, "max_seq_len": msl, "seed": args.seed,
                    "finalize": "mean weights and score feedback of each layer in the next layer's finalize launch"
                    if deferred else ("per layer: tt_engine_step" if cfg["mode"] == "step" else
                                      "per layer: tt_engine_ingest, then tt_engine_feedback with injected weights")},
@@ -494,7 +494,7 @@ def batch_bench(args, torch, L, lib):
         "dtype": "f32", "data": "synthetic (seeded N(0,1) on the GPU; packed by the library quantisers)",
         "config": {"workload": f"{args.config}: {B} sequences, ctx {ctxs}, {Hq} q heads / {Hkv} KV heads, head_dim "
                                f"{D}, {layers} layers, {args.meta} metadata, mean attention weights computed",
-                   "ctxs": ctxs, "layers": layers, "hip_graph": graphed},
+                   "ctxs": ctxs, "layers": layers, "hip_graph": graphed, "seed": args.seed},
         "achieved_GBps": round(gbps, 1),
         "pct_of_hbm_peak": round(100.0 * gbps / HBM_PEAK_GBPS, 2),
         "bytes_read_per_step": bstep,
@@ -795,7 +795,9 @@ def main():
         "vs_baseline": None,
         "dtype": "f32",
         "arithmetic": ARITHMETIC,
-        "data": "synthetic (seeded N(0,1) on the GPU, K outlier channels x8; packed by the library quantisers)",
+        "data": "synthetic (seeded N(0,1) on the GPU" + {"x8": ", 4 K outlier channels per KV head x8",
+                                                          "t3": ", 4 Student-t (nu=3) K outlier channels per KV head"}
+        .get(outl, "") + "; packed by the library quantisers)",
         "config": {
             "workload": f"{args.config}: decode attention over {layers} layers, batch 1, ctx {ctx}, "
                         f"{Hq} q heads / {Hkv} KV heads, head_dim {D}, 4 sinks + 256 recent + "
@@ -803,6 +805,7 @@ def main():
                         f"{args.meta} metadata, mean attention weights computed",
             "layers": layers, "ctx": ctx, "num_q_heads": Hq, "num_kv_heads": Hkv, "head_dim": D,
             "dense_tokens": nd, "packed_tokens": npk, "blocks": nb, "meta": args.meta, "hip_graph": graphed,
+            "seed": args.seed,
             "finalize": ("per layer: partials, then one launch merging this layer and computing the previous "
                          "layer's mean weights; the last layer's mean weights in a launch of their own")
             if deferred else "per layer: one fused call (partials, then merge and mean weights in one launch)",
