@@ -10,7 +10,8 @@
   (nu = 3) outlier channels, then decode steps in score-injected lockstep with
   the oracle engine (csrc/cache_engine.cpp:397-541) for 160 steps, across threshold refreshes
   over ~131k candidates and several waiting-room flushes: full state bit-exact
-  every 8 steps, attention against the oracle and against exact attention.
+  every 8 steps, attention against the oracle and against exact attention. The
+  same loop with 32-token blocks and f16 metadata over a 16k prefill.
 """
 import numpy as np
 import pytest
@@ -78,19 +79,28 @@ def _t3_keys(seed, stream, n, Hkv, D):
     return K
 
 
-def test_qwen2_128k_engine_lockstep(C, oracle):
-    Hq, Hkv, D, ctx, S, R, hr, decay, iv, kgs = 28, 4, 128, 131072, 4, 256, 0.05, 0.999, 32, 16
-    # The cached threshold is 0 until its first refresh 32 steps in (every eviction
-    # before that is promoted), and afterwards about a quarter of the evicted
-    # tokens (which collected feedback in the recent window) fall below it: 160
-    # steps cover four refreshes and two flushes.
-    steps = 160
-    msl = ctx + 320
-    seed = 55
-    eng = C.TriTierCacheEngine(Hq, Hkv, D, msl, S, R, hr, decay, iv, kgs, "fp32")
-    ls = Lockstep(oracle, Hq, Hkv, D, msl, S, R, hr, decay, iv, kgs, False)
+# (name, prefill tokens, steps, k_group_size, fp16 metadata, seed, waiting-room flushes at least)
+# The cached threshold is 0 until its first refresh 32 steps in (every eviction
+# before that is promoted), and afterwards about a quarter of the evicted tokens
+# (which collected feedback in the recent window) fall below it: 160 steps at
+# 131k cover four refreshes and two 16-token flushes; the seven-head groups
+# with 32-token blocks and f16 metadata (the 8-head matrix-core kernel's other
+# instantiation) run 260 steps over a 16k prefill.
+ENGINE_LOCKSTEP = [
+    ("qwen2-7b-128k", 131072, 160, 16, False, 55, 2),
+    ("gqa7-16k-kgs32-fp16", 16384, 260, 32, True, 56, 1),
+]
+
+
+@pytest.mark.parametrize("name,ctx,steps,kgs,fp16,seed,min_flushes", ENGINE_LOCKSTEP,
+                         ids=[c[0] for c in ENGINE_LOCKSTEP])
+def test_qwen2_engine_lockstep(C, oracle, name, ctx, steps, kgs, fp16, seed, min_flushes):
+    Hq, Hkv, D, S, R, hr, decay, iv = 28, 4, 128, 4, 256, 0.05, 0.999, 32
+    msl = ctx + 2 * steps
+    eng = C.TriTierCacheEngine(Hq, Hkv, D, msl, S, R, hr, decay, iv, kgs, "fp16" if fp16 else "fp32")
+    ls = Lockstep(oracle, Hq, Hkv, D, msl, S, R, hr, decay, iv, kgs, fp16)
     K, V = _t3_keys(seed, 1, ctx, Hkv, D), synth.normal(seed, 2, (ctx, Hkv, D))
-    print("prefill 131072 tokens", flush=True)
+    print(name, "prefill", ctx, "tokens", flush=True)
     eng.prefill(dev(K), dev(V), ctx)
     ls.prefill(K, V)
     del K, V
@@ -114,21 +124,21 @@ def test_qwen2_128k_engine_lockstep(C, oracle):
             # step's exact tier values, and to the oracle within 1e-4 plus the
             # oracle's own distance from that exact result.
             ls.oe.ingest(k, v)
-            xo, xmw = engine_exact_attention(oracle, ls.oe.state(), q, Hq, Hkv, D, kgs, False)
+            xo, xmw = engine_exact_attention(oracle, ls.oe.state(), q, Hq, Hkv, D, kgs, fp16)
             xo = xo.reshape(-1)
             ro, rmw = ls.oe.attend(q)
             ls.oe.feedback(g_mw)
             r = {"norm_vs_oracle": rel_err(g_out, ro), "oracle_vs_exact": rel_err(ro, xo),
                  "elem_vs_exact": elementwise_ratio(g_out, xo), "mw_rel_vs_exact": weights_rel_err(g_mw, xmw),
                  "mw_norm_vs_oracle": rel_err(g_mw, rmw), "oracle_mw_vs_exact": rel_err(rmw, xmw)}
-            print("step", s, {k_: f"{v_:.3g}" for k_, v_ in r.items()}, flush=True)
+            print(name, "step", s, {k_: f"{v_:.3g}" for k_, v_ in r.items()}, flush=True)
             assert r["elem_vs_exact"] <= 1.0 and r["mw_rel_vs_exact"] <= 1e-4, (s, r)
             assert r["norm_vs_oracle"] <= 1e-4 + r["oracle_vs_exact"], (s, r)
             assert r["mw_norm_vs_oracle"] <= 1e-4 + r["oracle_mw_vs_exact"], (s, r)
         if (s + 1) % 8 == 0:
             ls.check_state(eng, s)
     c1 = eng.counters()
-    print("counters after prefill", c0, "after steps", c1, flush=True)
-    # the loop crossed threshold refreshes over ~131k candidates and two flushes
+    print(name, "counters after prefill", c0, "after steps", c1, flush=True)
+    # the loop crossed threshold refreshes over every candidate and waiting-room flushes
     assert c1["last_calc_pos"] >= c0["total_processed_tokens"] + 32, (c0, c1)
-    assert c1["pbs_blocks_used"] >= c0["pbs_blocks_used"] + 2, (c0, c1)
+    assert c1["pbs_blocks_used"] >= c0["pbs_blocks_used"] + min_flushes, (c0, c1)
