@@ -96,7 +96,10 @@ TT_API int tt_dequantize_v(const int32_t* packed, const void* scale, const void*
  * holds for every attention entry point and for tt_engine_create's
  * max_seq_len).
  * Uses a library-owned device workspace (grown on demand, one per device);
- * concurrent calls on one device race on it -- use the _ws variant for that. */
+ * concurrent calls on one device race on it -- use the _ws variant for that.
+ * Growing it synchronises the device and frees the previous buffer, so a HIP
+ * graph captured around an earlier call must not be replayed after a call
+ * with a larger workspace (capture the _ws or _noalloc variant instead). */
 TT_API int tt_fused_attention_decode(const float* Q, const float* dense_K, const float* dense_V,
                               int dense_count, const int32_t* PBS_K_Packed,
                               const void* PBS_K_Scales, const void* PBS_K_Zeroes,
