@@ -4,13 +4,16 @@ tests/test_cache_init.py (TriTierCache construction), tests/test_wiring_verifica
 tests/test_multi_model_patch.py (the attention patch on tiny offline configs).
 Here every module and tensor lives on the ROCm device and the engine runs on it.
 
-TriTierCache.prefill/step and the patched attention of a LLaMA and a Qwen2
-layer (head_dim 128, GQA) also run in score-injected lockstep with the oracle
-engine: the post-RoPE Q/K/V each call hands the engine are fed to the oracle,
-the GPU's mean attention weights are its score feedback, the tier state must
-stay bit-exact and the context vector before o_proj must match the oracle's.
+TriTierCache.prefill/step and the patched attention of LLaMA, Mistral, Qwen2
+and Qwen3 layers (head_dim 128, GQA) also run in score-injected lockstep with
+the oracle engine: the post-RoPE Q/K/V each call hands the engine are fed to
+the oracle, the GPU's mean attention weights are its score feedback, the tier
+state must stay bit-exact and the context vector before o_proj must match the
+oracle's. The Q/K/V the patch hands the engine are checked against those the
+family's own unpatched forward computes for the same hidden states.
 """
 import math
+import sys
 
 import numpy as np
 import pytest
@@ -410,11 +413,13 @@ def _spy_lockstep(oracle, cache, every=50):
     prefill, step = cache.prefill, cache.step
 
     def spy_prefill(K, V):
+        log["prefill_kv"] = (K.clone(), V.clone())
         prefill(K, V)
         ls.prefill(host(K.float()), host(V.float()))
         ls.check_state(cache._engine, "prefill")
 
     def spy_step(Q, K, V, out):
+        log["step_qkv"] = (Q.clone(), K.clone(), V.clone())
         step(Q, K, V, out)
         r = ls.step(host(Q), host(K), host(V), host(out), host(cache._engine.get_mean_attn_weights()))
         log["errors"].append(r)
@@ -426,13 +431,17 @@ def _spy_lockstep(oracle, cache, every=50):
     return ls, log
 
 
-@pytest.mark.parametrize("arch", ["llama", "qwen2"])
+@pytest.mark.parametrize("arch", ["llama", "qwen2", "mistral", "qwen3"])
 def test_patched_attention_lockstep_with_oracle(patched, oracle, arch):
     """A patched LLaMA layer (8 q / 2 KV heads, head_dim 128, the patch's own lazily
-    created cache: 32k capacity, 256-token ring, f16 metadata) and a patched Qwen2
-    layer (14 q / 2 KV heads, head_dim 128, a 1024-token cache set on the module so
-    that its 52 heavy-hitter slots fill and demote): a 700-token prompt, then 300
-    decode steps, each in lockstep with the oracle engine."""
+    created cache: 32k capacity, 256-token ring, f16 metadata), likewise a Mistral
+    layer (16 q / 4 KV heads) and a Qwen3 layer (8 q / 2 KV heads, RMS-normed
+    queries and keys before the rotation), and a patched Qwen2 layer (14 q / 2 KV
+    heads, head_dim 128, a 1024-token cache set on the module so that its 52
+    heavy-hitter slots fill and demote): a 700-token prompt, then 300 decode
+    steps, each in lockstep with the oracle engine. The prompt's K/V and every
+    50th step's Q/K/V, as handed to the engine, equal the family's own unpatched
+    forward's."""
     import transformers as tf
 
     from tritiercache_amd.cache import TriTierCache
@@ -443,12 +452,29 @@ def test_patched_attention_lockstep_with_oracle(patched, oracle, arch):
 
         cfg = tf.LlamaConfig(hidden_size=1024, num_attention_heads=8, num_key_value_heads=2, head_dim=128,
                              max_position_embeddings=4096)
+    elif arch == "mistral":
+        from transformers.models.mistral.modeling_mistral import MistralAttention as A, MistralRotaryEmbedding as Rot
+
+        cfg = tf.MistralConfig(hidden_size=1024, num_attention_heads=16, num_key_value_heads=4, head_dim=128,
+                               max_position_embeddings=4096)
+    elif arch == "qwen3":
+        if not hasattr(tf, "Qwen3Config"):
+            pytest.skip("Qwen3 not in the installed transformers")
+        from transformers.models.qwen3.modeling_qwen3 import Qwen3Attention as A, Qwen3RotaryEmbedding as Rot
+
+        cfg = tf.Qwen3Config(hidden_size=1024, num_attention_heads=8, num_key_value_heads=2, head_dim=128,
+                             max_position_embeddings=4096)
     else:
         from transformers.models.qwen2.modeling_qwen2 import Qwen2Attention as A, Qwen2RotaryEmbedding as Rot
 
         cfg = tf.Qwen2Config(hidden_size=896, num_attention_heads=14, num_key_value_heads=2, head_dim=128,
                              max_position_embeddings=4096)
     layer, rot = A(cfg, layer_idx=0).to(DEV).eval(), Rot(config=cfg).to(DEV)
+    if arch == "qwen3":
+        # non-trivial norm weights, so that a patch that skipped the q/k norms would diverge
+        with torch.no_grad():
+            layer.q_norm.weight.uniform_(0.5, 1.5)
+            layer.k_norm.weight.uniform_(0.5, 1.5)
     if arch == "qwen2":
         layer.tri_tier_cache = TriTierCache(max_seq_len=1024, head_dim=128, num_heads=2, R_size=64, H_ratio=0.05,
                                             num_q_heads=14, score_decay=patched.SCORE_DECAY,
@@ -460,15 +486,47 @@ def test_patched_attention_lockstep_with_oracle(patched, oracle, arch):
         patched._layer_cache(layer, h0.device)
     cache = layer.tri_tier_cache
     ls, log = _spy_lockstep(oracle, cache)
+    family = sys.modules[A.__module__]
+    unpatched = patched._ORIGINAL_FORWARDS[A]
+
+    def family_qkv(h, pe):
+        """Post-RoPE Q/K/V [1, heads, tokens, D] as the family's own unpatched
+        forward computes them, taken at its call of the eager attention."""
+        got, eager, impl = {}, family.eager_attention_forward, cfg._attn_implementation
+
+        def capture(module, q, k, v, mask, **kw):
+            got["q"], got["k"], got["v"] = q, k, v
+            return eager(module, q, k, v, mask, **kw)
+
+        family.eager_attention_forward, cfg._attn_implementation = capture, "eager"
+        try:
+            unpatched(layer, h, position_embeddings=pe, attention_mask=None)
+        finally:
+            family.eager_attention_forward, cfg._attn_implementation = eager, impl
+        return got
+
+    def same(mine, theirs, what):
+        torch.testing.assert_close(mine, theirs.float(), rtol=1e-6, atol=1e-6, msg=lambda m: f"{arch} {what}: {m}")
+
     n0 = 700
     with torch.no_grad():
         h = torch.randn(1, n0, cfg.hidden_size, device=DEV)
-        layer(h, position_embeddings=rot(h, torch.arange(n0, device=DEV)[None]))
+        pe = rot(h, torch.arange(n0, device=DEV)[None])
+        layer(h, position_embeddings=pe)
+        ref = family_qkv(h, pe)
+        K, V = log["prefill_kv"]
+        same(K, ref["k"][0].transpose(0, 1), "prefill K")
+        same(V, ref["v"][0].transpose(0, 1), "prefill V")
         for s in range(300):
             h = torch.randn(1, 1, cfg.hidden_size, device=DEV)
-            out, _ = layer(h, position_embeddings=rot(h, torch.tensor([[n0 + s]], device=DEV)))
+            pe = rot(h, torch.tensor([[n0 + s]], device=DEV))
+            out, _ = layer(h, position_embeddings=pe)
             r = log["errors"][-1]
             assert attention_ok(r), (arch, s, r)
+            if s % 50 == 0:
+                ref = family_qkv(h, pe)
+                for mine, name in zip(log["step_qkv"], "qkv"):
+                    same(mine, ref[name].reshape(-1), f"step {s} {name.upper()}")
     assert log["steps"] == 300 and cache.Total_Processed_Tokens == n0 + 300
     ls.check_state(cache._engine, "end")
     worst = {k: max(e[k] for e in log["errors"]) for k in log["errors"][0]}
