@@ -439,9 +439,9 @@ def test_patched_attention_lockstep_with_oracle(patched, oracle, arch):
     queries and keys before the rotation), and a patched Qwen2 layer (14 q / 2 KV
     heads, head_dim 128, a 1024-token cache set on the module so that its 52
     heavy-hitter slots fill and demote): a 700-token prompt, then 300 decode
-    steps, each in lockstep with the oracle engine. The prompt's K/V and every
-    50th step's Q/K/V, as handed to the engine, equal the family's own unpatched
-    forward's."""
+    steps, each in lockstep with the oracle engine. The prompt's output (causal
+    attention) and K/V and every 50th step's Q/K/V, as handed to the engine,
+    equal the family's own unpatched forward's."""
     import transformers as tf
 
     from tritiercache_amd.cache import TriTierCache
@@ -512,7 +512,15 @@ def test_patched_attention_lockstep_with_oracle(patched, oracle, arch):
     with torch.no_grad():
         h = torch.randn(1, n0, cfg.hidden_size, device=DEV)
         pe = rot(h, torch.arange(n0, device=DEV)[None])
-        layer(h, position_embeddings=pe)
+        out, _ = layer(h, position_embeddings=pe)
+        # the prompt's output: causal attention, as the family's own SDPA path computes it
+        impl = cfg._attn_implementation
+        cfg._attn_implementation = "sdpa"
+        try:
+            want, _ = unpatched(layer, h, position_embeddings=pe, attention_mask=None)
+        finally:
+            cfg._attn_implementation = impl
+        torch.testing.assert_close(out, want, rtol=1e-5, atol=1e-5, msg=lambda m: f"{arch} prompt output: {m}")
         ref = family_qkv(h, pe)
         K, V = log["prefill_kv"]
         same(K, ref["k"][0].transpose(0, 1), "prefill K")
