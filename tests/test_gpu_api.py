@@ -370,6 +370,45 @@ def test_end_to_end_causal_lm_generate(patched):
     assert not hasattr(model.model.layers[0].self_attn, "tri_tier_cache")
 
 
+def test_causal_lm_logits_match_unpatched_model_while_tiers_are_fp32(patched):
+    """A two-layer LLaMA (8 q / 2 KV heads, head_dim 128), teacher-forced over a
+    40-token prompt and 200 decode tokens: with sinks + ring = 260 slots nothing is
+    evicted or quantised yet, so the engine's attention is exact float32
+    attention over every token, and the patched model's next-token logits must
+    match the unpatched model's (HF DynamicCache, SDPA) at every position."""
+    from transformers import DynamicCache, LlamaConfig, LlamaForCausalLM
+
+    cfg = LlamaConfig(vocab_size=512, hidden_size=1024, intermediate_size=2048, num_hidden_layers=2,
+                      num_attention_heads=8, num_key_value_heads=2, head_dim=128, max_position_embeddings=1024,
+                      pad_token_id=0, bos_token_id=1, eos_token_id=2)
+    torch.manual_seed(11)
+    model = LlamaForCausalLM(cfg).to(DEV).eval()
+    n0, n_dec = 40, 200
+    assert n0 + n_dec <= 4 + patched.R_SIZE  # every token stays in the FP32 sinks and ring
+    ids = torch.randint(3, cfg.vocab_size, (1, n0 + n_dec), device=DEV)
+
+    def run():
+        past = DynamicCache()
+        logits = [model(input_ids=ids[:, :n0], past_key_values=past, use_cache=True).logits[0, -1]]
+        for t in range(n0, n0 + n_dec - 1):
+            out = model(input_ids=ids[:, t:t + 1], position_ids=torch.tensor([[t]], device=DEV),
+                        past_key_values=past, use_cache=True)
+            logits.append(out.logits[0, -1])
+        return torch.stack(logits)
+
+    with torch.no_grad():
+        patched.remove_patch()
+        try:
+            want = run()
+        finally:
+            patched.apply_patch()
+        got = run()
+    c0 = model.model.layers[0].self_attn.tri_tier_cache
+    assert c0.Total_Processed_Tokens == n0 + n_dec - 1 and c0.PBS_count == 0 and c0.HH_count == 0
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=1e-4)
+    assert torch.equal(got.argmax(-1), want.argmax(-1))
+
+
 @pytest.mark.parametrize("arch", ["mistral", "qwen2", "qwen3"])
 def test_other_architectures_prefill_and_decode(patched, arch):
     import transformers as tf
