@@ -1,5 +1,5 @@
 """Float64 softmax attention over a tiered layer's exact values (test infrastructure only:
-the parity tests and bench.py's baseline leg use it as a checker).
+the parity tests and bench.py's baseline leg compare results against it).
 
 The FP32 dense rows are taken as they are and the packed rows as the oracle's
 bit-exact dequantisation (x = fmaf(q, scale, zero), csrc/cpu/dequantize_avx2.cpp
