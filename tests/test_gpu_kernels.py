@@ -466,3 +466,43 @@ def test_full_size_layer_vs_oracle(C, oracle, name, Hq, Hkv, ctx, fp16, outliers
     assert r["mw_norm_vs_oracle"] <= ATTN_TOL, (name, r)
     assert r["mw_rel_vs_oracle"] <= 1e-4 and r["mw_rel_vs_exact"] <= 1e-4, (name, r)
     assert abs(float(gmw.astype(np.float64).sum()) - 1.0) < 1e-3
+
+
+def test_library_workspace_grows_between_calls(C):
+    """tt_fused_attention_decode keeps one library-owned workspace per device and
+    grows it on demand (device synchronise, free, allocate). A small layer, then
+    one whose workspace exceeds every earlier call's (64 query heads over a
+    393,216-token layer: 96 MiB of logits), then the small layer again: every
+    output and mean-weight vector equals, bit for bit, the same call with a
+    caller-provided workspace (tt_fused_attention_decode_ws)."""
+    import ctypes
+
+    from tritiercache_amd import _lib
+
+    L = _lib.load()
+    D = 128
+    layers = [_tiered_layer(C, 8, 2, D, 2048, False, seed=61),
+              _tiered_layer(C, 64, 2, D, 393216, False, seed=62, k_outliers="x8")]
+    hq = [8, 64]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for i in (0, 1, 0):
+        Q, dK, dV, nd, blocks, ids, nb = layers[i]
+        Hq = hq[i]
+        n = nd + nb * 16
+        ptrs = [Q.data_ptr(), dK.data_ptr(), dV.data_ptr(), nd, *(b.data_ptr() for b in blocks), ids.data_ptr(), nb,
+                Hq, 2, D]
+        out_lib = torch.full((Hq, D), float("nan"), device="cuda")
+        mw_lib = torch.full((n,), float("nan"), device="cuda")
+        _lib.check(L.tt_fused_attention_decode(*ptrs, out_lib.data_ptr(), mw_lib.data_ptr(), 16, 0, stream),
+                   "fused_attention_decode")
+        ws_bytes = int(L.tt_fused_attention_workspace_bytes(nd, nb, Hq, 2, D, 16, 1))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device="cuda")
+        out_ws = torch.full_like(out_lib, float("nan"))
+        mw_ws = torch.full_like(mw_lib, float("nan"))
+        _lib.check(L.tt_fused_attention_decode_ws(*ptrs, out_ws.data_ptr(), mw_ws.data_ptr(), 16, 0, ws.data_ptr(),
+                                                  ws_bytes, stream), "fused_attention_decode_ws")
+        torch.cuda.synchronize()
+        assert torch.isfinite(out_lib).all() and torch.isfinite(mw_lib).all(), i
+        assert torch.equal(out_lib, out_ws) and torch.equal(mw_lib, mw_ws), (i, Hq, n)
+        if i == 1:
+            assert Hq * n * 4 >= 96 << 20
