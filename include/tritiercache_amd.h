@@ -269,7 +269,13 @@ TT_API int tt_engine_step(tt_engine* e, const float* Q, const float* K_new, cons
 /* step() plus the per-head softmax weights of this step, written as
  * [num_q_heads, visible] f32 in the engine's visible order (sinks, heavy-hitter
  * slots, recent window oldest first, packed slots). `visible_out` (host int)
- * receives the visible count; this call synchronises `stream`. */
+ * receives the visible count; this call synchronises `stream`.
+ * `head_weights_capacity` (columns per head row): the visible count before the
+ * step plus max(1, chunk_size) always suffices, as one step adds at most one
+ * visible token or one flushed block. A capacity that the step's visible count
+ * could exceed (by the engine's host-side tier bounds and by that count)
+ * returns TT_ERR_OUT_OF_RANGE before the step is enqueued, with the engine
+ * unchanged. */
 TT_API int tt_engine_step_weights(tt_engine* e, const float* Q, const float* K_new, const float* V_new,
                            float* attn_output, float* head_weights, int head_weights_capacity,
                            int* visible_out, void* stream);

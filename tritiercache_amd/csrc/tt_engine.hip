@@ -1069,16 +1069,50 @@ int tt_engine_flush_feedback(tt_engine* e, void* stream) {
     return engine_flush(e, as_stream(stream));
 }
 
+// Upper bound on the visible token count after the next ingest, from the
+// host-side tier bounds alone (no device read): the new token lands in the
+// sinks or the ring, or an eviction routes one token into the heavy hitters
+// (up to max_hh) or the waiting room, whose flush adds one block.
+static long long visible_ub_after_ingest(const tt_engine* e) {
+    long long s = e->h_s, rw = e->h_rw, hh = e->h_routed, blocks = e->blocks_ub;
+    if (s < e->S) {
+        ++s;
+    } else if (rw < e->R) {
+        ++rw;
+    } else {
+        if (hh < e->max_hh) ++hh;
+        if (e->wr_ub + 1 >= e->chunk) ++blocks;
+    }
+    return s + hh + rw + blocks * static_cast<long long>(e->chunk);
+}
+
 int tt_engine_step_weights(tt_engine* e, const float* Q, const float* K_new, const float* V_new, float* attn_output,
                            float* head_weights, int head_weights_capacity, int* visible_out, void* stream) {
     clear_error();
     if (!e) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "engine is NULL.");
     if (!Q || !attn_output || !head_weights)
         TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'Q'/'attn_output'/'head_weights' pointer address is NULL.");
-    int rc = tt_engine_ingest(e, K_new, V_new, stream);
-    if (rc) return rc;
+    if (!K_new || !V_new) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "Argument 'K_new'/'V_new' pointer address is NULL.");
     DeviceGuard dg(e->device);
     hipStream_t s = as_stream(stream);
+    // The capacity is validated before the step is enqueued, so a rejected call
+    // leaves the tiers as they were (bindings.cpp:120-128 validates before
+    // computing). The host-side bound needs no device read; when it does not
+    // fit, the device counters give the exact bound: one step adds at most one
+    // visible token, or one block of `chunk` tokens when the waiting room
+    // flushes.
+    if (visible_ub_after_ingest(e) > head_weights_capacity) {
+        int rc = engine_sync_state(e, s);
+        if (rc) return rc;
+        const int* st = e->host_state;
+        const long long vis_now = static_cast<long long>(st[kSCount]) + st[kHhCount] + st[kRwCount] +
+                                  static_cast<long long>(st[kBlocksUsed]) * e->chunk;
+        if (vis_now + std::max(1, e->chunk) > head_weights_capacity)
+            TT_FAIL(TT_ERR_OUT_OF_RANGE, "head_weights capacity is smaller than the step's visible token bound "
+                                         "(the visible tokens before the step plus one block).");
+    }
+    int rc = tt_engine_ingest(e, K_new, V_new, stream);
+    if (rc) return rc;
     rc = engine_attend(e, Q, attn_output, head_weights, head_weights_capacity, true, s);
     if (rc) return rc;
     rc = engine_sync_state(e, s);
