@@ -16,8 +16,12 @@ from __future__ import annotations
 import numpy as np
 
 
-def exact_attention(oracle, Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs=16, fp16=False):
-    """(out [Hq, D], mean weights [nd + nb * kgs]) in float64."""
+def exact_attention(oracle, Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs=16, fp16=False,
+                    per_head=False):
+    """(out [Hq, D], mean weights [nd + nb * kgs]) in float64; with per_head also the
+    per-head softmax weights [Hq, nd + nb * kgs] (0 at masked tokens), the weights
+    the reference's torch path returns for output_attentions
+    (src/tri_tier/integration/patch_model.py:33-51)."""
     G = Hq // Hkv
     parts_k, parts_v = [], []
     if nd:
@@ -32,8 +36,9 @@ def exact_attention(oracle, Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, 
     n = valid.size
     out = np.zeros((Hq, D))
     mw = np.zeros(n)
+    W = np.zeros((Hq, n))
     if n == 0:
-        return out, mw
+        return (out, mw, W) if per_head else (out, mw)
     K = np.concatenate(parts_k)
     V = np.concatenate(parts_v)
     q = np.asarray(Q, np.float32).reshape(Hq, D).astype(np.float64)
@@ -47,9 +52,10 @@ def exact_attention(oracle, Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, 
         L = p.sum(axis=1, keepdims=True)
         L[L == 0] = 1.0
         w = p / L
+        W[h * G:(h + 1) * G] = w
         out[h * G:(h + 1) * G] = w @ np.ascontiguousarray(V[:, h, :]).astype(np.float64)
         mw += w.sum(axis=0)
-    return out, mw / Hq
+    return (out, mw / Hq, W) if per_head else (out, mw / Hq)
 
 
 def elementwise_ratio(got, want, rtol=1e-4, atol_frac=1e-6) -> float:
@@ -68,7 +74,7 @@ def weights_rel_err(got, want, floor=1e-8) -> float:
     return float((np.abs(got[m] - want[m]) / want[m]).max()) if m.any() else 0.0
 
 
-def engine_exact_attention(oracle, state, Q, Hq, Hkv, D, kgs, fp16):
+def engine_exact_attention(oracle, state, Q, Hq, Hkv, D, kgs, fp16, per_head=False):
     """exact_attention over an engine's visible tokens, from a state dict (counters
     plus flat tier buffers, as oracle.binding.CpuEngine.state() returns): sinks,
     heavy-hitter slots, the recent window oldest first, then the used packed
@@ -90,4 +96,59 @@ def engine_exact_attention(oracle, state, Q, Hq, Hkv, D, kgs, fp16):
     VZ = np.asarray(state["PBS_V_Zeroes"]).reshape(-1, Hkv)[: nb * kgs]
     ids = np.asarray(state["PBS_token_ids"]).reshape(-1)[: nb * kgs]
     assert dK.size == (s + hh + rw) * kvs
-    return exact_attention(oracle, Q, dK, dV, s + hh + rw, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, fp16)
+    return exact_attention(oracle, Q, dK, dV, s + hh + rw, KP, KS, KZ, VP, VS, VZ, ids, nb, Hq, Hkv, D, kgs, fp16,
+                           per_head)
+
+
+def engine_visible_ids(state):
+    """Token id of every column of the engine's attention order (sinks, heavy-hitter
+    slots, recent window oldest first, packed slots), from a state dict."""
+    c = state["counters"]
+    s, hh, rw, nb, total = (c["s_count"], c["hh_count"], c["rw_count"], c["pbs_blocks_used"],
+                            c["total_processed_tokens"])
+    kgs = c["k_group_size"]
+    return np.concatenate([np.arange(s, dtype=np.int64), np.asarray(state["HH_token_ids"]).reshape(-1)[:hh],
+                           np.arange(total - rw, total, dtype=np.int64),
+                           np.asarray(state["PBS_token_ids"]).reshape(-1)[: nb * kgs]])
+
+
+def reconstruct_order(state):
+    """The permutation of the engine's attention order into the order of the
+    reference's reconstruct_full_cache (src/tri_tier/cache.py:326-372): sinks, then
+    heavy hitters and valid packed tokens sorted by token id, then the recent window
+    oldest first. Packed slots with id -1 are dropped."""
+    c = state["counters"]
+    s, hh, rw = c["s_count"], c["hh_count"], c["rw_count"]
+    ids = engine_visible_ids(state)
+    nd = s + hh + rw
+    middle = np.concatenate([np.arange(s, s + hh), np.arange(nd, ids.size)])
+    middle = middle[ids[middle] != -1]
+    middle = middle[np.argsort(ids[middle], kind="stable")]
+    return np.concatenate([np.arange(s), middle, np.arange(s + hh, nd)]).astype(np.int64)
+
+
+def reconstruct_full_cache(oracle, state, Hkv, D, fp16):
+    """(K, V, ids) in reconstruct_order, the packed rows through the oracle's
+    bit-exact dequantisers (csrc/cpu/dequantize_avx2.cpp)."""
+    c = state["counters"]
+    s, hh, rw, head, nb = c["s_count"], c["hh_count"], c["rw_count"], c["rw_head_index"], c["pbs_blocks_used"]
+    kgs = c["k_group_size"]
+    rows = lambda name: np.asarray(state[name]).reshape(-1, Hkv, D)  # noqa: E731
+    R = rows("RW_K").shape[0]
+    ring = (head + np.arange(rw)) % max(R, 1)
+    W = kgs // 16
+    parts_k = [rows("S_K")[:s], rows("HH_K")[:hh], rows("RW_K")[ring]]
+    parts_v = [rows("S_V")[:s], rows("HH_V")[:hh], rows("RW_V")[ring]]
+    if nb:
+        parts_k.append(oracle.dequantize_k(np.asarray(state["PBS_K_Packed"]).reshape(-1, W, Hkv, D)[:nb],
+                                           np.asarray(state["PBS_K_Scales"]).reshape(-1, Hkv, D)[:nb],
+                                           np.asarray(state["PBS_K_Zeroes"]).reshape(-1, Hkv, D)[:nb],
+                                           nb, Hkv, D, kgs, fp16))
+        parts_v.append(oracle.dequantize_v(np.asarray(state["PBS_V_Packed"]).reshape(-1, Hkv, (D + 15) // 16)[: nb * kgs],
+                                           np.asarray(state["PBS_V_Scales"]).reshape(-1, Hkv)[: nb * kgs],
+                                           np.asarray(state["PBS_V_Zeroes"]).reshape(-1, Hkv)[: nb * kgs],
+                                           nb * kgs, Hkv, D, fp16))
+    K = np.concatenate(parts_k)
+    V = np.concatenate(parts_v)
+    perm = reconstruct_order(state)
+    return K[perm], V[perm], engine_visible_ids(state)[perm]

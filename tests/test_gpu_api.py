@@ -19,7 +19,7 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_helpers import Lockstep, attention_ok, dev, host
+from gpu_helpers import Lockstep, attention_ok, dev, host, same_bits
 from oracle import synth
 
 pytestmark = pytest.mark.gpu
@@ -248,6 +248,166 @@ def test_cache_prefill_and_steps_lockstep_with_oracle(oracle, Hq, Hkv, kgs, meta
             ls.check_state(c._engine, s)
     assert c.HH_count == c.max_heavy_hitters
     assert c._engine.counters()["pbs_blocks_used"] >= blocks0 + 2
+
+
+# ---------------------------------------------------------------------------
+# Per-head weights and reconstruct_full_cache in lockstep with the oracle
+# (the reference's torch path, src/tri_tier/integration/patch_model.py:33-51,
+# returned at :162-169; src/tri_tier/cache.py:326-372)
+# ---------------------------------------------------------------------------
+def _check_weights_against_oracle(oracle, ls, q, w, ids, Hq, Hkv, D, kgs, fp16, tag):
+    """w [Hq, visible] and ids [visible] as step_with_weights returns them, against
+    float64 per-head softmax weights over the oracle engine's tiers (the tiers the
+    step attended: the score feedback changes no membership), permuted into
+    reconstruct order."""
+    from oracle.exact import engine_exact_attention, engine_visible_ids, reconstruct_order, weights_rel_err
+
+    st = ls.oe.state()
+    _, _, W = engine_exact_attention(oracle, st, q, Hq, Hkv, D, kgs, fp16, per_head=True)
+    perm = reconstruct_order(st)
+    assert np.array_equal(host(ids), engine_visible_ids(st)[perm]), tag
+    got = host(w).astype(np.float64)
+    want = W[:, perm]
+    assert got.shape == want.shape, (tag, got.shape, want.shape)
+    err = weights_rel_err(got, want)
+    assert err <= 1e-4, (tag, err)
+    assert np.abs(got.sum(axis=1) - 1.0).max() <= 1e-5, tag
+    return err
+
+
+def _check_reconstruct_against_oracle(oracle, ls, cache, fp16, tag):
+    from oracle.exact import reconstruct_full_cache
+
+    K, V, ids = cache.reconstruct_full_cache()
+    oK, oV, oids = reconstruct_full_cache(oracle, ls.oe.state(), cache.num_heads, cache.head_dim, fp16)
+    assert np.array_equal(host(ids), oids), tag
+    assert same_bits(host(K), oK) and same_bits(host(V), oV), tag
+    # every visible token in id order, and nothing but the waiting room left out
+    assert np.all(np.diff(oids) > 0), tag
+    assert oids.size == cache.Total_Processed_Tokens - cache.WR_count, tag
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,kgs,meta", [(8, 2, 128, 16, "fp16"), (12, 4, 64, 32, "fp32"),
+                                               (28, 4, 128, 16, "fp32")])
+def test_step_with_weights_and_reconstruct_lockstep_with_oracle(oracle, Hq, Hkv, D, kgs, meta):
+    """A 400-token prefill and 200 decode steps through TriTierCache in score-injected
+    lockstep with the oracle engine (heavy hitters filling and demoting, waiting-room
+    flushes): every fifth step through step_with_weights, whose per-head weights
+    (reconstruct order) must equal float64 softmax weights over the oracle's tiers
+    within 1e-4 relative for every weight >= 1e-8, with the same token ids; every
+    40 steps reconstruct_full_cache() must equal the oracle's dequantised tiers bit
+    for bit."""
+    from tritiercache_amd.cache import TriTierCache
+
+    fp16 = meta == "fp16"
+    c = TriTierCache(max_seq_len=1024, head_dim=D, num_heads=Hkv, R_size=64, H_ratio=0.05, num_q_heads=Hq,
+                     k_group_size=kgs, pbs_metadata_dtype=meta)
+    ls = _lockstep_for(oracle, c)
+    seed = 700 + Hq + D
+    Kp, Vp = synth.normal(seed, 1, (400, Hkv, D)), synth.normal(seed, 2, (400, Hkv, D))
+    c.prefill(dev(Kp), dev(Vp))
+    ls.prefill(Kp, Vp)
+    _check_reconstruct_against_oracle(oracle, ls, c, fp16, "prefill")
+    worst, checked = 0.0, 0
+    for s in range(200):
+        q = synth.normal(seed, 10 + 3 * s, (Hq * D,))
+        k, v = synth.normal(seed, 11 + 3 * s, (Hkv * D,)), synth.normal(seed, 12 + 3 * s, (Hkv * D,))
+        out = torch.empty(Hq * D, dtype=torch.float32, device=DEV)
+        with_w = s % 5 == 0 or s == 199
+        if with_w:
+            w, ids = c.step_with_weights(dev(q), dev(k), dev(v), out)
+        else:
+            c.step(dev(q), dev(k), dev(v), out)
+        r = ls.step(q, k, v, host(out), host(c._engine.get_mean_attn_weights()))
+        assert attention_ok(r), (s, r)
+        if with_w:
+            worst = max(worst, _check_weights_against_oracle(oracle, ls, q, w, ids, Hq, Hkv, D, kgs, fp16, s))
+            checked += 1
+        if (s + 1) % 40 == 0:
+            _check_reconstruct_against_oracle(oracle, ls, c, fp16, s)
+            ls.check_state(c._engine, s)
+    assert checked == 41
+    assert c.HH_count == c.max_heavy_hitters and c.PBS_count > 0
+    print(f"per-head weights worst rel err {worst:.3g} over {checked} steps", flush=True)
+
+
+@pytest.mark.parametrize("kgs,meta", [(16, "fp16"), (32, "fp32")])
+def test_live_cache_bytes_equal_the_engine_buffers_in_use(kgs, meta):
+    """accounting.live_cache_bytes prices the tiers from the engine's counters; each
+    tier's figure equals the bytes of the device buffers that tier occupies (sinks,
+    ring, heavy-hitter rows + ids + scores, packed words, scales/zeros + ids, the
+    waiting room's rows), and the canonical measure_cache_bytes of the same cache
+    object takes its shapes from it."""
+    from tritiercache_amd.accounting import live_cache_bytes, measure_cache_bytes
+    from tritiercache_amd.cache import TriTierCache
+
+    Hq, Hkv, D = 8, 2, 128
+    c = TriTierCache(max_seq_len=2048, head_dim=D, num_heads=Hkv, R_size=64, H_ratio=0.05, num_q_heads=Hq,
+                     k_group_size=kgs, pbs_metadata_dtype=meta)
+    c.prefill(torch.randn(500, Hkv, D, device=DEV), torch.randn(500, Hkv, D, device=DEV))
+    out = torch.empty(Hq * D, device=DEV)
+    for _ in range(150):
+        c.step(torch.randn(Hq * D, device=DEV), torch.randn(Hkv * D, device=DEV), torch.randn(Hkv * D, device=DEV),
+               out)
+    cnt = c._engine.counters()
+    s, rw, hh, wr, nb, npk = (cnt[k] for k in ("s_count", "rw_count", "hh_count", "wr_count", "pbs_blocks_used",
+                                               "pbs_count"))
+    assert hh > 0 and nb > 0 and wr > 0 and npk == nb * kgs
+    nbytes = lambda t: t.numel() * t.element_size()  # noqa: E731
+    r = live_cache_bytes(c, num_layers=3)
+    assert r["sink_bytes"] == 3 * (nbytes(c.S_K_Buffer[:s]) + nbytes(c.S_V_Buffer[:s]))
+    assert r["rw_bytes"] == 3 * (nbytes(c.RW_K_Buffer[:rw]) + nbytes(c.RW_V_Buffer[:rw]))
+    assert r["hh_bytes"] == 3 * (nbytes(c.HH_K_Buffer[:hh]) + nbytes(c.HH_V_Buffer[:hh]) +
+                                 nbytes(c.HH_token_ids[:hh]) + nbytes(c.HH_scores[:hh]))
+    assert r["pbs_payload_bytes"] == 3 * (nbytes(c.PBS_K_Packed[:nb]) + nbytes(c.PBS_V_Packed[:npk]))
+    assert r["pbs_metadata_bytes"] == 3 * (nbytes(c.PBS_K_Scales[:nb]) + nbytes(c.PBS_K_Zeroes[:nb]) +
+                                           nbytes(c.PBS_V_Scales[:npk]) + nbytes(c.PBS_V_Zeroes[:npk]) +
+                                           nbytes(c.PBS_token_ids[:npk]))
+    assert r["wr_bytes"] == 3 * (nbytes(c.WR_K_Buffer[:wr]) + nbytes(c.WR_V_Buffer[:wr]))
+    assert r["actual_sinks"] + r["actual_rw"] + r["actual_hh"] + r["actual_pbs"] + r["actual_wr"] == 650
+    canon = measure_cache_bytes(cache_obj=c, num_layers=3, k_group_size=kgs, pbs_metadata_dtype=meta)
+    assert (canon["num_kv_heads"], canon["head_dim"], canon["total_tokens"]) == (Hkv, D, 650)
+
+
+def test_step_with_weights_rejects_small_capacity_before_the_step():
+    """A head-weights capacity the step could exceed is rejected (IndexError in
+    Python) before anything is enqueued: the engine's state is unchanged. A capacity
+    of the visible count plus one block is always accepted."""
+    import ctypes as C
+
+    from gpu_helpers import gpu_engine_state
+    from tritiercache_amd import _C, _lib
+
+    Hq, Hkv, D = 8, 2, 64
+    eng = _C.TriTierCacheEngine(Hq, Hkv, D, 512, 4, 16, 0.1, 0.999, 32, 16, "fp16")
+    eng.prefill(torch.randn(100, Hkv, D, device=DEV), torch.randn(100, Hkv, D, device=DEV), 100)
+    for _ in range(5):
+        eng.step(torch.randn(Hq * D, device=DEV), torch.randn(Hkv * D, device=DEV),
+                 torch.randn(Hkv * D, device=DEV), torch.empty(Hq * D, device=DEV))
+    before = gpu_engine_state(eng)
+    vis = eng.visible()
+    q, k, v = (torch.randn(n, device=DEV) for n in (Hq * D, Hkv * D, Hkv * D))
+    out = torch.full((Hq * D,), 7.0, device=DEV)
+    w = torch.zeros((Hq, vis + 16), device=DEV)
+    got = C.c_int(-1)
+    for cap in (1, vis):  # below every bound of the step's visible count
+        rc = _lib.load().tt_engine_step_weights(eng._h, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                                w.data_ptr(), cap, C.byref(got), None)
+        assert rc == _lib.TT_ERR_OUT_OF_RANGE, rc
+        assert "capacity" in _lib.last_error()
+    torch.cuda.synchronize()
+    assert got.value == -1 and torch.all(out == 7.0) and torch.all(w == 0)
+    after = gpu_engine_state(eng)
+    assert after["counters"] == before["counters"]
+    for name in before:
+        if name != "counters":
+            assert same_bits(after[name], before[name]), name
+    # the bound itself is accepted
+    rc = _lib.load().tt_engine_step_weights(eng._h, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                                            w.data_ptr(), vis + 16, C.byref(got), None)
+    assert rc == _lib.TT_OK and 0 < got.value <= vis + 16
+    torch.cuda.synchronize()
+    assert torch.allclose(w[:, : got.value].sum(dim=1), torch.ones(Hq, device=DEV), atol=1e-5)
 
 
 # ---------------------------------------------------------------------------
@@ -581,3 +741,65 @@ def test_patched_attention_lockstep_with_oracle(patched, oracle, arch):
           cache._engine.counters()["pbs_blocks_used"], flush=True)
     if arch == "qwen2":
         assert cache.HH_count == cache.max_heavy_hitters
+
+
+def test_patched_attention_weights_lockstep_with_oracle(patched, oracle):
+    """A patched LLaMA layer (8 q / 2 KV heads, head_dim 128, a 1024-token cache with
+    f16 metadata set on the module) called with output_attentions=True for every
+    one of 150 decode steps after a 400-token prompt: each step's (1, Hq, 1, visible)
+    weights -- the reference returns per-head softmax weights over the
+    reconstructed cache there (patch_model.py:33-51, :162-169) -- equal float64
+    softmax weights over the oracle engine's tiers, in reconstruct order, within
+    1e-4 relative for every weight >= 1e-8; the engine runs in score-injected
+    lockstep with the oracle (state bit-exact every 50 steps) and the last step's
+    reconstruct_full_cache() equals the oracle's."""
+    import transformers as tf
+    from transformers.models.llama.modeling_llama import LlamaAttention as A, LlamaRotaryEmbedding as Rot
+
+    from tritiercache_amd.cache import TriTierCache
+
+    torch.manual_seed(9)
+    cfg = tf.LlamaConfig(hidden_size=1024, num_attention_heads=8, num_key_value_heads=2, head_dim=128,
+                         max_position_embeddings=4096)
+    Hq, Hkv, D = 8, 2, 128
+    layer, rot = A(cfg, layer_idx=0).to(DEV).eval(), Rot(config=cfg).to(DEV)
+    layer.tri_tier_cache = TriTierCache(max_seq_len=1024, head_dim=D, num_heads=Hkv, R_size=64, H_ratio=0.05,
+                                        num_q_heads=Hq, score_decay=patched.SCORE_DECAY,
+                                        k_group_size=patched.K_GROUP_SIZE,
+                                        pbs_metadata_dtype=patched.PBS_METADATA_DTYPE)
+    cache = layer.tri_tier_cache
+    fp16 = cache.pbs_metadata_dtype == "fp16"
+    ls = _lockstep_for(oracle, cache)
+    log = {}
+    prefill, step_w = cache.prefill, cache.step_with_weights
+
+    def spy_prefill(K, V):
+        prefill(K, V)
+        ls.prefill(host(K.float()), host(V.float()))
+
+    def spy_step_w(Q, K, V, out):
+        w, ids = step_w(Q, K, V, out)
+        log["r"] = ls.step(host(Q), host(K), host(V), host(out), host(cache._engine.get_mean_attn_weights()))
+        log["q"], log["ids"] = host(Q), ids
+        return w, ids
+
+    cache.prefill, cache.step_with_weights = spy_prefill, spy_step_w
+    n0, worst = 400, 0.0
+    with torch.no_grad():
+        h = torch.randn(1, n0, cfg.hidden_size, device=DEV)
+        layer(h, position_embeddings=rot(h, torch.arange(n0, device=DEV)[None]))
+        ls.check_state(cache._engine, "prefill")
+        for s in range(150):
+            h = torch.randn(1, 1, cfg.hidden_size, device=DEV)
+            out, w = layer(h, position_embeddings=rot(h, torch.tensor([[n0 + s]], device=DEV)),
+                           output_attentions=True)
+            assert out.shape == (1, 1, cfg.hidden_size)
+            assert attention_ok(log["r"]), (s, log["r"])
+            assert w.shape == (1, Hq, 1, cache.Total_Processed_Tokens - cache.WR_count), (s, w.shape)
+            worst = max(worst, _check_weights_against_oracle(oracle, ls, log["q"], w[0, :, 0], log["ids"], Hq, Hkv,
+                                                             D, cache.k_group_size, fp16, s))
+            if (s + 1) % 50 == 0:
+                ls.check_state(cache._engine, s)
+    _check_reconstruct_against_oracle(oracle, ls, cache, fp16, "end")
+    assert cache.HH_count > 0 and cache.PBS_count > 0
+    print(f"patched layer per-head weights worst rel err {worst:.3g}", flush=True)

@@ -268,6 +268,65 @@ def test_engine_exact_attention_matches_oracle_engine(oracle):
     assert np.abs(rmw - xmw).max() <= 1e-6 * xmw.max()
 
 
+def test_reconstruct_order_and_rows_from_the_inputs(oracle):
+    """oracle.exact.reconstruct_full_cache / reconstruct_order (the order of the
+    reference's reconstruct_full_cache, src/tri_tier/cache.py:326-372) pinned by the
+    inputs themselves, after a run with a wrapped ring, heavy hitters and flushed
+    blocks: the ids are every processed token except the waiting room's, strictly
+    increasing; each FP32-tier row is the K/V row that token was given, bit for bit;
+    each packed row is within half a quantisation step of it; and the per-head
+    weights in that order are the engine-order weights permuted (rows sum to 1)."""
+    from oracle.exact import engine_exact_attention, engine_visible_ids, reconstruct_full_cache, reconstruct_order
+
+    cfg = engine_runs.RUNS["step_gqa_d128_fp16"]
+    Hq, Hkv, D, kgs, fp16 = cfg["Hq"], cfg["Hkv"], cfg["D"], cfg["kgs"], cfg["fp16"]
+    e = oracle.engine(*engine_runs.engine_args(cfg))
+    K0, V0 = engine_runs.prefill_inputs(cfg)
+    e.prefill(K0, V0)
+    Ks, Vs = [np.asarray(K0).reshape(-1, Hkv, D)], [np.asarray(V0).reshape(-1, Hkv, D)]
+    for s in range(150):
+        Q, K, V = engine_runs.step_inputs(cfg, s)
+        e.step(Q, K, V)
+        Ks.append(np.asarray(K).reshape(1, Hkv, D))
+        Vs.append(np.asarray(V).reshape(1, Hkv, D))
+    Kin, Vin = np.concatenate(Ks), np.concatenate(Vs)
+    st = e.state()
+    c = st["counters"]
+    assert c["hh_count"] > 0 and c["pbs_blocks_used"] > 0 and c["rw_head_index"] > 0 and c["wr_count"] > 0
+    K, V, ids = reconstruct_full_cache(oracle, st, Hkv, D, fp16)
+    wr = set(np.asarray(st["WR_token_ids"]).reshape(-1)[: c["wr_count"]].tolist())
+    total = c["total_processed_tokens"]
+    assert total == Kin.shape[0]
+    assert ids.tolist() == [t for t in range(total) if t not in wr]
+    hh = set(np.asarray(st["HH_token_ids"]).reshape(-1)[: c["hh_count"]].tolist())
+    nb = c["pbs_blocks_used"]
+    slot = {t: j for j, t in enumerate(np.asarray(st["PBS_token_ids"]).reshape(-1)[: nb * kgs].tolist())}
+    meta = (lambda a: np.asarray(a).view(np.float16).astype(np.float32)) if fp16 else np.asarray  # noqa: E731
+    KS, KZ = meta(st["PBS_K_Scales"]).reshape(-1, Hkv, D), meta(st["PBS_K_Zeroes"]).reshape(-1, Hkv, D)
+    VS, VZ = meta(st["PBS_V_Scales"]).reshape(-1, Hkv, 1), meta(st["PBS_V_Zeroes"]).reshape(-1, Hkv, 1)
+
+    def half_step(sc, z):
+        # codes are chosen with the float32 scale/min; f16 metadata rounds both
+        return 0.5 * sc + 2.0 ** -10 * (3 * sc + np.abs(z)) + 1e-6
+
+    n_packed = 0
+    for i, t in enumerate(ids.tolist()):
+        if t in slot:
+            assert t not in hh
+            j = slot[t]
+            assert np.all(np.abs(K[i] - Kin[t]) <= half_step(KS[j // kgs], KZ[j // kgs])), t
+            assert np.all(np.abs(V[i] - Vin[t]) <= half_step(VS[j], VZ[j])), t
+            n_packed += 1
+        else:
+            assert np.array_equal(K[i], Kin[t]) and np.array_equal(V[i], Vin[t]), t
+    assert n_packed == nb * kgs
+    Q, _, _ = engine_runs.step_inputs(cfg, 150)
+    _, _, W = engine_exact_attention(oracle, st, Q, Hq, Hkv, D, kgs, fp16, per_head=True)
+    perm = reconstruct_order(st)
+    assert np.array_equal(engine_visible_ids(st)[perm], ids)
+    assert np.allclose(W[:, perm].sum(axis=1), 1.0, atol=1e-12)
+
+
 @pytest.mark.parametrize("fp16,kgs,Hq,Hkv,D,msl,R,hr", [(True, 16, 4, 2, 64, 256, 16, 0.1),
                                                        (False, 16, 32, 8, 128, 4096, 256, 0.05),
                                                        (True, 32, 28, 4, 128, 2000, 64, 0.02),
