@@ -30,12 +30,15 @@ def is_gpu_supported() -> bool:
     return HAS_CPP_EXT and _C.device_count() > 0
 
 
+from .accounting import live_cache_bytes, measure_cache_bytes  # noqa: E402
 from .cache import TriTierCache  # noqa: E402
 
 __version__ = "0.1.0"
 
 __all__ = [
     "TriTierCache",
+    "measure_cache_bytes",
+    "live_cache_bytes",
     "DEVICE",
     "UPDATE_THRESHOLD",
     "CHUNK_SIZE",
