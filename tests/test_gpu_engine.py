@@ -15,7 +15,7 @@ import torch
 
 import engine_runs
 from oracle import synth
-from gpu_helpers import dev, gpu_engine_state, gpu_state_digest, host, rel_err, same_bits
+from gpu_helpers import attention_ok, dev, gpu_engine_state, gpu_state_digest, host, rel_err, same_bits
 
 pytestmark = pytest.mark.gpu
 ATTN_TOL = 1e-4
@@ -311,3 +311,52 @@ def test_deferred_feedback_chain_matches_per_layer_steps(C, Hq, Hkv, D, kgs, fp1
     Q = dev(synth.normal(1, 0, (Hq, D)))
     assert L.tt_engine_step_deferred(B[0]._h, Q.data_ptr(), Q.data_ptr(), Q.data_ptr(), ob.data_ptr(), B[0]._h,
                                      stream()) == 1
+
+
+@pytest.mark.parametrize("Hq,Hkv,D,kgs,fp16", [(8, 2, 128, 16, False), (28, 4, 128, 16, True), (4, 1, 64, 32, False)])
+def test_deferred_feedback_chain_lockstep_with_oracle(C, oracle, Hq, Hkv, D, kgs, fp16):
+    """Three engines stepped as a model's layers with tt_engine_step_deferred (each engine's mean weights and
+    score feedback in the next engine's finalize launch, the last one flushed), each beside an oracle engine in
+    score-injected lockstep: the oracle is fed the deferred mean weights the GPU engine used for its own
+    feedback. 220 steps after a 300-token prompt, through ring overflow, threshold refreshes (every 16 tokens),
+    heavy-hitter promotions and waiting-room flushes: each layer's output and mean weights
+    within the attention tolerance of the oracle's at every step, and the full state (counters, every tier
+    buffer, the score vector) bit-exact every 20 steps."""
+    from gpu_helpers import Lockstep
+    from tritiercache_amd import _lib
+
+    L = _lib.load()
+    layers, msl, prompt, steps, R, hr, decay, iv = 3, 720, 300, 220, 64, 0.1, 0.99, 16
+    meta = "fp16" if fp16 else "fp32"
+    E = [C.TriTierCacheEngine(Hq, Hkv, D, msl, 4, R, hr, decay, iv, kgs, meta) for _ in range(layers)]
+    LS = [Lockstep(oracle, Hq, Hkv, D, msl, 4, R, hr, decay, iv, kgs, fp16) for _ in range(layers)]
+    for i in range(layers):
+        K, V = synth.normal(7200 + i, 0, (prompt, Hkv, D)), synth.normal(7300 + i, 0, (prompt, Hkv, D))
+        tK, tV = dev(K), dev(V)  # held until the prefill is enqueued
+        E[i].prefill(tK.data_ptr(), tV.data_ptr(), prompt)
+        LS[i].prefill(K, V)
+    stream = lambda: torch.cuda.current_stream().cuda_stream  # noqa: E731
+    outs = [torch.empty((Hq, D), device="cuda") for _ in range(layers)]
+    worst = {}
+    for s in range(steps):
+        inputs = []
+        for i in range(layers):
+            q = synth.normal(8200 + 10 * s + i, 0, (Hq * D,))
+            k, v = synth.normal(9200 + 10 * s + i, 0, (Hkv * D,)), synth.normal(9700 + 10 * s + i, 0, (Hkv * D,))
+            inputs.append((q, k, v))
+            tq, tk, tv = dev(q), dev(k), dev(v)
+            prev = E[i - 1]._h if i > 0 else None
+            _lib.check(L.tt_engine_step_deferred(E[i]._h, tq.data_ptr(), tk.data_ptr(), tv.data_ptr(),
+                                                 outs[i].data_ptr(), prev, stream()), "step_deferred")
+        _lib.check(L.tt_engine_flush_feedback(E[-1]._h, stream()), "flush")
+        for i in range(layers):
+            q, k, v = inputs[i]
+            r = LS[i].step(q, k, v, host(outs[i]).reshape(-1), host(E[i].get_mean_attn_weights()))
+            assert attention_ok(r), (s, i, r)
+            for key, val in r.items():
+                worst[key] = max(worst.get(key, 0.0), val)
+            if s % 20 == 19:
+                LS[i].check_state(E[i], (s, i))
+    c = E[0].counters()
+    assert c["hh_count"] > 0 and c["pbs_blocks_used"] > prompt // kgs and c["last_calc_pos"] > prompt, c
+    print("deferred chain worst", {k: f"{v:.3g}" for k, v in worst.items()}, flush=True)
