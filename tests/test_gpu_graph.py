@@ -13,7 +13,8 @@ import pytest
 import torch
 
 from oracle import synth
-from gpu_helpers import dev, host, rel_err, same_bits
+from gpu_helpers import attention_errors, attention_ok, dev, host, rel_err, same_bits
+from oracle.exact import weights_rel_err
 import test_gpu_kernels as K
 
 pytestmark = pytest.mark.gpu
@@ -237,6 +238,11 @@ def test_split_finalize_on_two_streams(lib, oracle, Hq, Hkv, D, nd, nb, kgs, fp1
         torch.cuda.synchronize()
         assert same_bits(host(out), host(r_out))
         assert np.abs(host(mw) - host(r_mw)).max() <= 1e-6 * np.abs(host(r_mw)).max()
+        # elementwise, like every other mean-weight check: against the fused call and the oracle
+        assert weights_rel_err(host(mw), host(r_mw)) <= 1e-5
+        ro, rmw = oracle.fused_attention_decode(host(t["Q"]), *args[1:])
+        err = attention_errors(host(out), ro, host(mw), rmw)
+        assert attention_ok(err), err
 
     out = torch.full((Hq, D), float("nan"), device="cuda")
     mw = torch.full((n,), float("nan"), device="cuda")
@@ -277,7 +283,7 @@ def test_deferred_mean_weights_across_layers(lib, oracle, Hq, Hkv, D, kgs, fp16,
         (Q, dK, dV, nd, KP, KS, KZ, VP, VS, VZ, ids, nb) = args[:12]
         t = {k: dev(v) for k, v in dict(Q=Q, dK=dK, dV=dV, KP=KP, KS=KS, KZ=KZ, VP=VP, VS=VS, VZ=VZ, ids=ids).items()}
         n = nd + nb * kgs
-        t.update(nd=nd, nb=nb, out=torch.empty((Hq, D), device="cuda"), mw=torch.empty((n,), device="cuda"),
+        t.update(nd=nd, nb=nb, args=args, out=torch.empty((Hq, D), device="cuda"), mw=torch.empty((n,), device="cuda"),
                  rout=torch.empty((Hq, D), device="cuda"), rmw=torch.empty((n,), device="cuda"))
         layers.append(t)
     ws_bytes = max(int(L.tt_fused_attention_workspace_bytes(t["nd"], t["nb"], Hq, Hkv, D, kgs, 1)) for t in layers)
@@ -320,6 +326,11 @@ def test_deferred_mean_weights_across_layers(lib, oracle, Hq, Hkv, D, kgs, fp16,
             assert same_bits(host(t["out"]), host(t["rout"])), (tag, i)
             r = host(t["rmw"])
             assert np.abs(host(t["mw"]) - r).max() <= 1e-6 * np.abs(r).max(), (tag, i)
+            # elementwise, like every other mean-weight check: against the fused call and the oracle
+            assert weights_rel_err(host(t["mw"]), r) <= 1e-5, (tag, i)
+            ro, rmw = oracle.fused_attention_decode(host(t["Q"]), *t["args"][1:])
+            err = attention_errors(host(t["out"]), ro, host(t["mw"]), rmw)
+            assert attention_ok(err), (tag, i, err)
 
     for t in layers:
         t["out"].fill_(float("nan"))

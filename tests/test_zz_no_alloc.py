@@ -83,3 +83,50 @@ def test_noalloc_rejects_oversized_call_on_host(lib):
     # the workspace query agrees that this call is above the limit
     assert lib.tt_fused_attention_workspace_bytes(0, 300000 // 16, 32, 8, 128, 16, 1) > (32 << 20)
     torch.cuda.synchronize()
+
+
+def test_noalloc_graph_replay_without_mean_weights_and_no_memory_growth(lib, oracle):
+    """After a warm-up call, (1) calls with and without mean weights (NULL) leave the
+    device's free memory unchanged, and (2) the call captured in a graph and replayed
+    with new queries matches the allocating entry point bit for bit on every replay,
+    with eager calls and synchronisations between the replays."""
+    from oracle import synth
+
+    case = make_case(oracle, 32, 8, 128, 300, 120, 16, False, "tail", 703)
+    a = _args(case)
+    n_tok = a["nd"] + a["nb"] * a["kgs"]
+    out = torch.empty((a["Hq"], a["D"]), dtype=torch.float32, device="cuda")
+    mw = torch.empty((n_tok,), dtype=torch.float32, device="cuda")
+    assert _call(lib.tt_fused_attention_decode_noalloc, a, out, mw) == 0, lib.tt_last_error()
+    torch.cuda.synchronize()
+    free0, _ = torch.cuda.mem_get_info()
+    out2 = torch.empty_like(out)
+    for m in (None, mw, None):
+        assert _call(lib.tt_fused_attention_decode_noalloc, a, out2, m) == 0, lib.tt_last_error()
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    assert same_bits(host(out2), host(out))  # the output does not depend on whether weights are asked for
+
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            rc = lib.tt_fused_attention_decode_noalloc(
+                _ptr(a["Q"]), _ptr(a["dK"]), _ptr(a["dV"]), a["nd"], _ptr(a["KP"]), _ptr(a["KS"]), _ptr(a["KZ"]),
+                _ptr(a["VP"]), _ptr(a["VS"]), _ptr(a["VZ"]), _ptr(a["ids"]), a["nb"], a["Hq"], a["Hkv"], a["D"],
+                _ptr(out), _ptr(mw), a["kgs"], a["fp16"], ctypes.c_void_p(s.cuda_stream))
+    torch.cuda.current_stream().wait_stream(s)
+    assert rc == 0, lib.tt_last_error()
+    for r in range(3):
+        a["Q"].copy_(dev(synth.normal(704 + r, 0, (a["Hq"], a["D"]))))
+        out.fill_(float("nan"))
+        mw.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        got_out, got_mw = host(out), host(mw)
+        (o_ref, mw_ref), (o_na, mw_na) = _both(lib, a)  # eager calls of both entry points between replays
+        assert same_bits(got_out, o_ref) and same_bits(got_mw, mw_ref), r
+        assert same_bits(o_na, o_ref) and same_bits(mw_na, mw_ref), r
+    del g
+    torch.cuda.synchronize()

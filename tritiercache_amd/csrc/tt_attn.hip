@@ -478,6 +478,16 @@ __device__ __forceinline__ float wave_sum(float x) {
 // the accumulators of splits g, g + groups, ... (up to kMergeU per group and
 // block of 256 splits, all in flight together).
 constexpr int kMergeU = 16;
+
+// The (m, l) statistics of two consecutive splits. A head's row starts at
+// 2 * h * nsplit floats and a pair at an even split only when nsplit is even,
+// so the pair is read as two 8-byte loads rather than one 16-byte load.
+__device__ __forceinline__ float4 load_ml_pair(const float* p) {
+    const float2 a = *reinterpret_cast<const float2*>(p);
+    const float2 b = *reinterpret_cast<const float2*>(p + 2);
+    return make_float4(a.x, a.y, b.x, b.y);
+}
+
 __device__ __forceinline__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
@@ -713,7 +723,7 @@ __device__ __forceinline__ void fin_mean_tokens(const FinArgs& a, const int wg, 
         for (int u = 0; u < kU4; ++u) {
             const int j = 2 * j0 + 16 * u;
             const int jj = j < a.nsplit - 2 ? j : a.nsplit - 2;
-            w[u] = *reinterpret_cast<const float4*>(ml + 2 * jj);
+            w[u] = load_ml_pair(ml + 2 * jj);
         }
         fin_load_logits_nb<MT, NU>(a, hg, wg * MT + 4 * q, n, lgv);
         __builtin_amdgcn_sched_barrier(0);  // keep both sets of loads ahead of the fold
@@ -752,7 +762,7 @@ __device__ __forceinline__ void fin_mean_tokens(const FinArgs& a, const int wg, 
             for (int u = 0; u < kU4; ++u) {
                 const int j = jb + 16 * u;
                 if (j + 1 < a.nsplit) {
-                    const float4 w = *reinterpret_cast<const float4*>(ml + 2 * j);
+                    const float4 w = load_ml_pair(ml + 2 * j);
                     v[2 * u] = make_float2(w.x, w.y);
                     v[2 * u + 1] = make_float2(w.z, w.w);
                 } else {

@@ -107,9 +107,34 @@ def _rotated_qkv(module, hidden_states, position_embeddings):
         k = module.k_norm(k)
     q, k, v = q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2)
     cos, sin = position_embeddings
-    rope = sys.modules[type(module).__module__].apply_rotary_pos_emb
-    q, k = rope(q, k, cos, sin)
+    rope = _family_rope(type(module))
+    if rope is not None:
+        q, k = rope(q, k, cos, sin)
+    else:
+        q, k = _rotate_half_rope(q, cos, sin), _rotate_half_rope(k, cos, sin)
     return q, k, v
+
+
+def _family_rope(cls):
+    """The ``apply_rotary_pos_emb`` of the model file that defines the patched
+    family class ``cls`` derives from (found through the MRO, so a subclass from
+    another module, e.g. remote code, uses its family's), or None."""
+    for base in cls.__mro__:
+        if base in _SUPPORTED_ATTENTION_CLASSES or base is cls:
+            fn = getattr(sys.modules.get(base.__module__), "apply_rotary_pos_emb", None)
+            if fn is not None:
+                return fn
+    return None
+
+
+def _rotate_half_rope(x, cos, sin):
+    """x * cos + rotate_half(x) * sin with cos/sin [1, q_len, D] broadcast over the
+    heads, the rotation the reference applies inline (patch_model.py:104-116)."""
+    if cos.ndim == 3:
+        cos, sin = cos.unsqueeze(1), sin.unsqueeze(1)
+    half = x.shape[-1] // 2
+    rot = torch.cat((-x[..., half:], x[..., :half]), dim=-1)
+    return x * cos + rot * sin
 
 
 def patched_forward(self, hidden_states: torch.Tensor,
