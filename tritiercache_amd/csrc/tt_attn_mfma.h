@@ -105,8 +105,8 @@ struct MfLds {
 // per-wave partials [4][GP][max, sum, acc[128]].
 template <int GP>
 struct DnLds {
-    static constexpr int QL = 0;
-    static constexpr int PART = GP * kMfD * 4;
+    static constexpr int QL = 0;                 // [16][128] f32: one row per MFMA column, zeros past the group
+    static constexpr int PART = 16 * kMfD * 4;
     static constexpr int TOTAL = PART + 4 * GP * (2 + kMfD) * 4;
 };
 
@@ -134,16 +134,6 @@ __device__ __forceinline__ float xrow_max(float x) {
 __device__ __forceinline__ float xrow_sum(float x) {
     const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     x = __uint_as_float(s[0]) + __uint_as_float(s[1]);
-    const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(t[0]) + __uint_as_float(t[1]);
-}
-// x[l] + x[l ^ 16]
-__device__ __forceinline__ float xrow_pair_sum(float x) {
-    const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
-}
-// x[l] + x[l ^ 32]
-__device__ __forceinline__ float xhalf_sum(float x) {
     const auto t = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
     return __uint_as_float(t[0]) + __uint_as_float(t[1]);
 }
@@ -343,158 +333,188 @@ __device__ __forceinline__ DenseView dense_view(const AttnInputs& in) {
     return v;
 }
 
-// Keys and values of one 16-token FP32 tile for one lane: the four tokens of
-// token group tg = lane / 16, channels 8 cp .. 8 cp + 7 (cp = lane % 16).
+// One 16-token FP32 tile for one lane (g = lane / 16, n = lane % 16) in the
+// operand layouts of v_mfma_f32_16x16x4_f32:
+//   k: keys of token n, channels 32 g .. 32 g + 31 (QK A operand, row n);
+//   v: values of tokens 4 g + j (j = 0..3), channels 8 n .. 8 n + 7 (PV B
+//      operand, column n of output block b holding channel 8 n + b).
 struct DenseTile {
-    float kx[4][8], vx[4][8];
+    float4 k[8];
+    float4 v[4][2];
 };
 
-// Issues the loads of tile k (logical order sinks -> heavy hitters -> recent
-// ring). Rows past the tiers repeat the last row (finite data, masked later).
+// K and V rows of token `r0` (clamped to the last tier row; rows past the
+// tiers are masked later) in the logical FP32 order sinks -> heavy hitters ->
+// recent ring.
+struct DenseRow {
+    const float* k;
+    const float* v;
+};
+__device__ __forceinline__ DenseRow dense_row(const AttnInputs& in, const DenseView& dv, const int kvh, const int r0) {
+    const int r = r0 < dv.Nd ? r0 : dv.Nd - 1;
+    const bool in0 = r < dv.n0, in1 = r < dv.n0 + dv.n1;
+    int ring = dv.head + (r - dv.n0 - dv.n1);
+    ring = ring >= in.ring_size ? ring - in.ring_size : ring;
+    const int idx = in0 ? r : (in1 ? r - dv.n0 : ring);
+    const float* kb = in0 ? in.k0 : (in1 ? in.k1 : in.k2);
+    const float* vb = in0 ? in.v0 : (in1 ? in.v1 : in.v2);
+    const size_t off = (static_cast<size_t>(idx) * in.Hkv + kvh) * kMfD;
+    return DenseRow{kb + off, vb + off};
+}
+
+// Issues the loads of tile k.
 __device__ __forceinline__ void dense_load(const AttnInputs& in, const DenseView& dv, const int kvh, const int k,
                                            DenseTile& t) {
     const int lane = threadIdx.x & 63;
-    const int tg = lane >> 4, cp = lane & 15;
-    const int tok0 = 16 * k + 4 * tg;
+    const int g = lane >> 4, n = lane & 15;
+    const int tok0 = 16 * k;
+    {
+        const float* kb = dense_row(in, dv, kvh, tok0 + n).k + 32 * g;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r0 = tok0 + i;
-        const int r = r0 < dv.Nd ? r0 : dv.Nd - 1;
-        const bool in0 = r < dv.n0, in1 = r < dv.n0 + dv.n1;
-        int ring = dv.head + (r - dv.n0 - dv.n1);
-        ring = ring >= in.ring_size ? ring - in.ring_size : ring;
-        const int idx = in0 ? r : (in1 ? r - dv.n0 : ring);
-        const float* kb = in0 ? in.k0 : (in1 ? in.k1 : in.k2);
-        const float* vb = in0 ? in.v0 : (in1 ? in.v1 : in.v2);
-        const size_t off = (static_cast<size_t>(idx) * in.Hkv + kvh) * kMfD + cp * 8;
-        load_f32<8>(kb + off, t.kx[i]);
-        load_f32<8>(vb + off, t.vx[i]);
+        for (int i = 0; i < 8; ++i) t.k[i] = *reinterpret_cast<const float4*>(kb + 4 * i);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float* vb = dense_row(in, dv, kvh, tok0 + 4 * g + j).v + 8 * n;
+        t.v[j][0] = *reinterpret_cast<const float4*>(vb);
+        t.v[j][1] = *reinterpret_cast<const float4*>(vb + 4);
     }
 }
 
-// FP32 tiers of the workgroup's share (16-token tiles [d0, d1)), VALU.
-// Wave w takes tiles d0 + w, d0 + w + 4, ...; the caller has
-// already issued the loads of the first one into `t0`, the others are loaded
-// as they come (a wave rarely has more than one). Lanes are (token group
-// tg = lane / 16) x (8-channel slice cp = lane % 16), the query heads of the
-// group in passes of up to four, read from the workgroup's copy of Q in LDS
-// (`q_l`, [GP][128]). Leaves one (max, sum, acc[128]) partial per head in `dl`
-// ([GP][2 + 128] per wave) and writes the dense logits.
+// Component r (a constant after unrolling) of a float4, and that component
+// scaled (values, not references, so the accumulators stay in registers).
+__device__ __forceinline__ float f4_get(const float4 v, const int r) {
+    return r == 0 ? v.x : (r == 1 ? v.y : (r == 2 ? v.z : v.w));
+}
+__device__ __forceinline__ float4 f4_scale(const float4 v, const int r, const float f) {
+    return make_float4(r == 0 ? v.x * f : v.x, r == 1 ? v.y * f : v.y, r == 2 ? v.z * f : v.z, r == 3 ? v.w * f : v.w);
+}
+
+__device__ __forceinline__ float4 mfma4x4f32(const float a, const float b, const float4 c) {
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v r = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, f4v{c.x, c.y, c.z, c.w}, 0, 0, 0);
+    return make_float4(r[0], r[1], r[2], r[3]);
+}
+
+// FP32 tiers of the workgroup's share (16-token tiles [d0, d1)) on the
+// matrix cores in f32 (v_mfma_f32_16x16x4_f32: the tier values are the
+// operands as they are stored). Wave w takes tiles d0 + w, d0 + w + 4, ...;
+// the caller has already issued the loads of the first one into `t0`.
+//   QK: D[token][head] = sum_c K[token][c] Q[head][c], channels 32 g + i of
+//       MFMA i in lane group g; lane (g, n) receives the logits of tokens
+//       4 g .. 4 g + 3 for head n (columns past the group's heads are unused).
+//   PV: O[head][c] = sum_t P[head][t] V[t][c], MFMA (j, b) over the tokens
+//       4 g + j (k = g), whose A operand is the QK result's register j as it
+//       lies, and channel 8 n + b in column n; lane (g, n) accumulates heads
+//       4 g .. 4 g + 3, channels 8 n + b.
+// Softmax online in log2 units with a lazy reference: a head's reference
+// moves only when a tile's maximum passes it by more than 16 (f32 holds the
+// 2^16 factor), so most tiles skip the rescale. Leaves one (max, sum,
+// acc[128]) partial per head in `dl` ([GP][2 + 128] per wave) and writes
+// the logits.
 template <int GP>
 __device__ __forceinline__ void dense_share(const SplitArgs& a, const DenseView& dv, const int d0, const int d1,
                                             const int kvh, const int g0, const int gc, const int wave,
                                             const float* q_l, const DenseTile& t0, float* dl) {
-    constexpr int HP = GP < 4 ? GP : 4;
-    constexpr int NPASS = GP / HP;
+    static_assert(GP <= 16, "one MFMA column per query head");
+    constexpr float kTau = 16.0f;
     const AttnInputs& in = a.in;
     const int lane = threadIdx.x & 63;
-    const int tg = lane >> 4, cp = lane & 15;
+    const int g = lane >> 4, n = lane & 15;
     const int G = in.Hq / in.Hkv;
     const int Nd = dv.Nd;
-    float* my = dl + wave * GP * (2 + kMfD);
-    // Heads [gb, gb + HP); the first pass starts with the prefetched tile.
-    // (Peeling that pass keeps `t0` out of the later passes' live range.)
-    auto run_pass = [&](const int gb, const bool first) {
-        float m[HP], l[HP], acc[HP][8];
+    float4 acc[8];
 #pragma unroll
-        for (int g = 0; g < HP; ++g) {
-            m[g] = kNegInf;
-            l[g] = 0.0f;
+    for (int b = 0; b < 8; ++b) acc[b] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    float m_run = kNegInf, l_run = 0.0f;
+    auto consume = [&](const DenseTile& t, const int k) {
+        const int tok0 = 16 * k + 4 * g;
+        // read per tile (an opaque offset keeps the compiler from holding
+        // the 32 query values over the loop)
+        int qo = n * kMfD + 32 * g;
+        asm volatile("" : "+v"(qo));
+        const float* qrow = q_l + qo;
+        float4 d = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
+        for (int i = 0; i < 8; ++i) {
+            const float4 qb = *reinterpret_cast<const float4*>(qrow + 4 * i);
+            d = mfma4x4f32(t.k[i].x, qb.x, d);
+            d = mfma4x4f32(t.k[i].y, qb.y, d);
+            d = mfma4x4f32(t.k[i].z, qb.z, d);
+            d = mfma4x4f32(t.k[i].w, qb.w, d);
         }
-        // One tile into the running (m, l, acc) of the pass's heads.
-        auto consume = [&](const DenseTile& t, const int k) {
-            const int tok0 = 16 * k + 4 * tg;
-            float s[4][HP];
+        float sv[4] = {d.x * a.scale2, d.y * a.scale2, d.z * a.scale2, d.w * a.scale2};
 #pragma unroll
-            for (int g = 0; g < HP; ++g) {
-                // read here, one head at a time (an opaque offset keeps the
-                // compiler from holding all heads in registers)
-                int qo = (gb + g) * kMfD + cp * 8;
-                asm volatile("" : "+v"(qo));
-                const float4 qa = *reinterpret_cast<const float4*>(q_l + qo);
-                const float4 qb = *reinterpret_cast<const float4*>(q_l + qo + 4);
-                const float qg[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+        for (int r = 0; r < 4; ++r) sv[r] = (tok0 + r < Nd) ? sv[r] : kNegInf;
+        if (a.logits && n < gc) {
+            float* lr = a.logits + static_cast<size_t>(kvh * G + g0 + n) * a.ld + tok0;
+            if (tok0 + 4 <= Nd) {
+                st_dev4(a.logits, static_cast<uint32_t>(in.Hq) * a.ld * 4u, static_cast<uint32_t>((lr - a.logits) * 4),
+                        make_float4(sv[0], sv[1], sv[2], sv[3]));
+            } else {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    float d = 0.0f;
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) d = __builtin_fmaf(qg[j], t.kx[i][j], d);
-                    const float v = row_sum16(d) * a.scale2;
-                    s[i][g] = (tok0 + i < Nd) ? v : kNegInf;
-                }
+                for (int r = 0; r < 4; ++r)
+                    if (tok0 + r < Nd) lr[r] = sv[r];
             }
-            if (a.logits) {
-#pragma unroll
-                for (int g = 0; g < HP; ++g) {
-                    if (gb + g < gc && cp == g) {
-                        float* lr = a.logits + static_cast<size_t>(kvh * G + g0 + gb + g) * a.ld + tok0;
-                        if (tok0 + 4 <= Nd) {
-                            st_dev4(a.logits, static_cast<uint32_t>(a.in.Hq) * a.ld * 4u,
-                                    static_cast<uint32_t>((lr - a.logits) * 4),
-                                    make_float4(s[0][g], s[1][g], s[2][g], s[3][g]));
-                        } else {
-#pragma unroll
-                            for (int i = 0; i < 4; ++i)
-                                if (tok0 + i < Nd) lr[i] = s[i][g];
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int g = 0; g < HP; ++g) {
-                float tm = fmaxf(fmaxf(s[0][g], s[1][g]), fmaxf(s[2][g], s[3][g]));
-                tm = xrow_max(tm);
-                const float mn = fmaxf(m[g], tm);
-                const float alpha = (m[g] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(m[g] - mn);
-                float p[4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) p[i] = (s[i][g] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(s[i][g] - mn);
-                l[g] = __builtin_fmaf(l[g], alpha, (p[0] + p[1]) + (p[2] + p[3]));
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    float v = acc[g][j] * alpha;
-                    v = __builtin_fmaf(p[0], t.vx[0][j], v);
-                    v = __builtin_fmaf(p[1], t.vx[1][j], v);
-                    v = __builtin_fmaf(p[2], t.vx[2][j], v);
-                    v = __builtin_fmaf(p[3], t.vx[3][j], v);
-                    acc[g][j] = v;
-                }
-                m[g] = mn;
-            }
-        };
-        int kb = d0 + wave;
-        if (first && kb < d1) {
-            consume(t0, kb);  // in flight since the start of the kernel
-            kb += 4;
         }
-#pragma unroll 1
-        for (int k = kb; k < d1; k += 4) {
-            DenseTile t;
-            dense_load(in, dv, kvh, k, t);
-            consume(t, k);
-        }
-        // Sum the four row groups (they share m) and leave the partial in LDS.
+        // the head's maximum over the tile (the four lane groups of column n)
+        const float hm = xrow_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3])));
+        if (__ballot(hm > m_run + kTau)) {
+            const bool up = hm > m_run + kTau;
+            const float mn = up ? hm : m_run;
+            const float al = (m_run == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(m_run - mn);
+            l_run *= al;
+            // accumulator row r of lane group g is head 4 g + r, whose factor
+            // sits in column 4 g + r
 #pragma unroll
-        for (int g = 0; g < HP; ++g) {
-            const float lt = xrow_sum(l[g]);
+            for (int r = 0; r < 4; ++r) {
+                const float ar = __shfl(al, 4 * g + r, 64);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) acc[g][j] = xrow_sum(acc[g][j]);
-            if (gb + g < GP && tg == 0) {
-                float* pg = my + (gb + g) * (2 + kMfD);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) pg[2 + cp * 8 + j] = acc[g][j];
-                if (cp == 0) {
-                    pg[0] = m[g];
-                    pg[1] = lt;
-                }
+                for (int b = 0; b < 8; ++b) acc[b] = f4_scale(acc[b], r, ar);
             }
+            m_run = mn;
+        }
+        float pv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pv[r] = (sv[r] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(sv[r] - m_run);
+        l_run += (pv[0] + pv[1]) + (pv[2] + pv[3]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float vv[8] = {t.v[j][0].x, t.v[j][0].y, t.v[j][0].z, t.v[j][0].w,
+                                 t.v[j][1].x, t.v[j][1].y, t.v[j][1].z, t.v[j][1].w};
+#pragma unroll
+            for (int b = 0; b < 8; ++b) acc[b] = mfma4x4f32(pv[j], vv[b], acc[b]);
         }
     };
-    run_pass(0, true);
+    int kb = d0 + wave;
+    if (kb < d1) {
+        consume(t0, kb);  // in flight since the start of the kernel
+        kb += 4;
+    }
 #pragma unroll 1
-    for (int pass = 1; pass < NPASS; ++pass) run_pass(pass * HP, false);
+    for (int k = kb; k < d1; k += 4) {
+        DenseTile t;
+        dense_load(in, dv, kvh, k, t);
+        consume(t, k);
+    }
+    // The head's sum over its four lane groups, then the partial in LDS:
+    // lane (0, h) holds (m, l) of head h, lane (g, n) the accumulators of
+    // heads 4 g + r, channels 8 n .. 8 n + 7.
+    l_run = xrow_sum(l_run);
+    float* my = dl + wave * GP * (2 + kMfD);
+    if (g == 0 && n < GP) {
+        my[n * (2 + kMfD)] = m_run;
+        my[n * (2 + kMfD) + 1] = l_run;
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int h = 4 * g + r;
+        if (h < GP) {
+            float* pg = my + h * (2 + kMfD) + 2 + 8 * n;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) pg[b] = f4_get(acc[b], r);
+        }
+    }
 }
 
 // One FP32-tier workgroup: KV head kvh, query heads [GP * chunk, +GP), FP32
@@ -514,14 +534,14 @@ __device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit,
     dense_range(a, dv.Nd, dsplit, d0, d1);
     float* q_l = reinterpret_cast<float*>(lds + L::QL);
     float* dl = reinterpret_cast<float*>(lds + L::PART);
-    load_q_lds<GP>(in, kvh, g0, gc, q_l);
-    DenseTile dt;
+    load_q_lds<16>(in, kvh, g0, gc, q_l);  // rows past the group's heads are zeros
     if (a.dense_delay > 0) {
         // bounded by the constant-rate real-time counter
         const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
         while (__builtin_amdgcn_s_memrealtime() - t0 < static_cast<unsigned long long>(a.dense_delay))
             __builtin_amdgcn_s_sleep(8);
     }
+    DenseTile dt;
     if (d0 + wave < d1) dense_load(in, dv, kvh, d0 + wave, dt);
     __syncthreads();
     dense_share<GP>(a, dv, d0, d1, kvh, g0, gc, wave, q_l, dt, dl);
@@ -1083,63 +1103,91 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         l_run += dpp<0x124>(l_run);
         pz += dpp<0x124>(pz);
     }
-    // rows h + 8 (low parts, lanes 32..63) onto rows h (lanes 0..31)
-#pragma unroll
-    for (int s = 0; s < 8; ++s)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[s][r] = xhalf_sum(acc[s][r]);
-    if constexpr (TP) {
-        // rows 4 + h (tile 1, lanes 16..31) onto rows h (lanes 0..15)
-#pragma unroll
-        for (int s = 0; s < 8; ++s)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[s][r] = xrow_pair_sum(acc[s][r]);
-    }
 
+    // Merge of the four waves through LDS. Lane (g = lane / 16, n = lane % 16)
+    // holds rows 4 g .. 4 g + 3 of the PV output, column n of each of the
+    // eight MFMAs: row 4 g + r is head r of tile g & 1 (high parts g < 2, low
+    // parts g >= 2) with packed tiles, else head (4 g + r) & 7 (high parts
+    // g < 2). Every lane stores its raw accumulators (channels 4 n + 64 q ..
+    // + 3 as one 16-byte write per (row, q)) and the merge threads add the
+    // row groups of a head and the waves in one pass, instead of reducing
+    // across lanes first.
+    constexpr int RR = GP < 4 ? GP : 4;                  // rows of a group that hold heads
+    constexpr int NGI = TP ? 4 : 2 * ((GP + 3) / 4);     // row groups that hold heads
+    constexpr int XW = NGI * RR * kMfD;                  // floats per wave
+    static_assert(4 * XW * 4 + 3 * 4 * GP * 4 <= 4 * L::BYTES, "merge area must fit in the staging area");
     __syncthreads();  // every wave is done with its staging area
-    float* sm_m = reinterpret_cast<float*>(lds);  // [4][GP]
+    float* sm_x = reinterpret_cast<float*>(lds);  // [4 waves][NGI][RR][128]
+    float* sm_m = sm_x + 4 * XW;                   // [4][GP]
     float* sm_l = sm_m + 4 * GP;                   // [4][GP]
     float* sm_z = sm_l + 4 * GP;                   // [4][GP]
-    float* sm_acc = sm_z + 4 * GP;                 // [4][GP][128]
     // The lane's indices again, from an opaque copy of the thread id: held
     // over the loop instead, they would cost registers the loop needs.
     int tx = static_cast<int>(threadIdx.x);
     asm volatile("" : "+v"(tx));
-    const int lane_e = tx & 63, n_e = tx & 15, gk_e = (tx >> 4) & 3;
+    const int lane_e = tx & 63, n_e = tx & 15, g_e = (tx >> 4) & 3;
     if (lane_e < GP) {
         sm_m[wave * GP + lane_e] = m_run;
         sm_l[wave * GP + lane_e] = l_run;
         sm_z[wave * GP + lane_e] = pz;
     }
-    if (lane_e < 32) {
+    {
+        // row group g_e -> slot gi (TP: all four; else the high group of
+        // heads 4 (g & 1) .. and the low group of the same heads)
+        const int gi = TP ? g_e : ((g_e & 1) + (g_e >> 1) * (NGI / 2));
+        const bool keep = TP || ((g_e & 1) < NGI / 2);
+        if (keep) {
+            float* xw = sm_x + wave * XW + gi * RR * kMfD + 4 * n_e;
 #pragma unroll
-        for (int s = 0; s < 8; ++s)
+            for (int r = 0; r < RR; ++r)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int h = 4 * gk_e + r;
-                if (h < GP) {
-                    const int c = 4 * n_e + 64 * (s >> 2) + (s & 3);
-                    sm_acc[(wave * GP + h) * kMfD + c] = __builtin_amdgcn_ldexpf(acc[s][r], -2 * (s & 3) - 1);
-                }
-            }
+                for (int q = 0; q < 2; ++q)
+                    *reinterpret_cast<float4*>(xw + r * kMfD + 64 * q) =
+                        make_float4(acc[4 * q][r], acc[4 * q + 1][r], acc[4 * q + 2][r], acc[4 * q + 3][r]);
+        }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < gc * kMfD; idx += 256) {
-        const int g = idx / kMfD, c = idx - g * kMfD;
+    // Thread (head h, channels 4 c4 .. 4 c4 + 3). The codes were scaled by
+    // 4^(c & 3) and centred as 2 q - 3, so channel c's sum carries 2^(2 (c & 3) + 1).
+    for (int idx = threadIdx.x; idx < gc * (kMfD / 4); idx += 256) {
+        const int h = idx / (kMfD / 4), c4 = idx - h * (kMfD / 4);
         float M = -1.0e30f;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w * GP + g]);
-        float A = 0.0f, Ls = 0.0f;
+        for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w * GP + h]);
+        float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        float Ls = 0.0f, Z = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             // a wave without pairs has m = -1e30, l = 0, acc = 0: it adds nothing
-            const float f = __builtin_amdgcn_exp2f(sm_m[w * GP + g] - M);
-            A = __builtin_fmaf(f, sm_acc[(w * GP + g) * kMfD + c] + sm_z[w * GP + g], A);
-            Ls = __builtin_fmaf(f, sm_l[w * GP + g], Ls);
+            const float f = __builtin_amdgcn_exp2f(sm_m[w * GP + h] - M);
+            const float* xw = sm_x + w * XW + 4 * c4;
+            float4 S;
+            if constexpr (TP) {
+                const float4 x0 = *reinterpret_cast<const float4*>(xw + (0 * RR + h) * kMfD);
+                const float4 x1 = *reinterpret_cast<const float4*>(xw + (1 * RR + h) * kMfD);
+                const float4 x2 = *reinterpret_cast<const float4*>(xw + (2 * RR + h) * kMfD);
+                const float4 x3 = *reinterpret_cast<const float4*>(xw + (3 * RR + h) * kMfD);
+                S = make_float4((x0.x + x1.x) + (x2.x + x3.x), (x0.y + x1.y) + (x2.y + x3.y),
+                                (x0.z + x1.z) + (x2.z + x3.z), (x0.w + x1.w) + (x2.w + x3.w));
+            } else {
+                const int gh = h >> 2, r = h & 3;
+                const float4 x0 = *reinterpret_cast<const float4*>(xw + (gh * RR + r) * kMfD);
+                const float4 x1 = *reinterpret_cast<const float4*>(xw + ((NGI / 2 + gh) * RR + r) * kMfD);
+                S = make_float4(x0.x + x1.x, x0.y + x1.y, x0.z + x1.z, x0.w + x1.w);
+            }
+            A.x = __builtin_fmaf(f, S.x, A.x);
+            A.y = __builtin_fmaf(f, S.y, A.y);
+            A.z = __builtin_fmaf(f, S.z, A.z);
+            A.w = __builtin_fmaf(f, S.w, A.w);
+            Z = __builtin_fmaf(f, sm_z[w * GP + h], Z);
+            Ls = __builtin_fmaf(f, sm_l[w * GP + h], Ls);
         }
-        const size_t pi = static_cast<size_t>(kvh * G + g0 + g) * a.nsplit + split;
-        st_dev1(a.part_acc + pi * kMfD + c, A);
-        if (c == 0) {
+        A = make_float4(__builtin_fmaf(A.x, 0.5f, Z), __builtin_fmaf(A.y, 0.125f, Z),
+                        __builtin_fmaf(A.z, 0.03125f, Z), __builtin_fmaf(A.w, 0.0078125f, Z));
+        const size_t pi = static_cast<size_t>(kvh * G + g0 + h) * a.nsplit + split;
+        st_dev4(a.part_acc, static_cast<uint32_t>(static_cast<size_t>(in.Hq) * a.nsplit * kMfD * 4u),
+                static_cast<uint32_t>((pi * kMfD + 4 * c4) * 4), A);
+        if (c4 == 0) {
             st_dev1(a.part_ml + 2 * pi, (Ls > 0.0f) ? M : kNegInf);
             st_dev1(a.part_ml + 2 * pi + 1, Ls);
         }
