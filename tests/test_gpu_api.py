@@ -609,7 +609,7 @@ def _spy_lockstep(oracle, cache, every=50):
     weights as score feedback; collects the attention errors of each step."""
     ls = _lockstep_for(oracle, cache)
     log = {"steps": 0, "errors": []}
-    prefill, step = cache.prefill, cache.step
+    prefill, step = cache.prefill, cache.step_deferred
 
     def spy_prefill(K, V):
         log["prefill_kv"] = (K.clone(), V.clone())
@@ -617,16 +617,18 @@ def _spy_lockstep(oracle, cache, every=50):
         ls.prefill(host(K.float()), host(V.float()))
         ls.check_state(cache._engine, "prefill")
 
-    def spy_step(Q, K, V, out):
+    def spy_step(Q, K, V, out, prev=None):
+        # the patch chains its decode steps (step_deferred); reading the mean
+        # weights runs this step's pending feedback first
         log["step_qkv"] = (Q.clone(), K.clone(), V.clone())
-        step(Q, K, V, out)
+        step(Q, K, V, out, prev=prev)
         r = ls.step(host(Q), host(K), host(V), host(out), host(cache._engine.get_mean_attn_weights()))
         log["errors"].append(r)
         log["steps"] += 1
         if log["steps"] % every == 0:
             ls.check_state(cache._engine, log["steps"])
 
-    cache.prefill, cache.step = spy_prefill, spy_step
+    cache.prefill, cache.step_deferred = spy_prefill, spy_step
     return ls, log
 
 
@@ -803,3 +805,73 @@ def test_patched_attention_weights_lockstep_with_oracle(patched, oracle):
     _check_reconstruct_against_oracle(oracle, ls, cache, fp16, "end")
     assert cache.HH_count > 0 and cache.PBS_count > 0
     print(f"patched layer per-head weights worst rel err {worst:.3g}", flush=True)
+
+
+def test_patched_layers_chain_deferred_steps_lockstep_with_oracle(patched, oracle):
+    """Two patched LLaMA layers (8 q / 2 KV heads, head_dim 128, 1024-token caches)
+    stepped as a model steps them: every decode step of layer 1 runs layer 0's pending
+    mean weights and score feedback in its finalize launch (the patch chains its steps
+    with step_deferred). Each layer's engine runs in score-injected lockstep with its
+    own oracle engine, fed the mean weights the GPU used -- read only after the next
+    layer's step, so layer 0's come from layer 1's launch -- through a 400-token prompt
+    and 250 decode steps: contexts within the attention tolerance, state bit-exact
+    every 50 steps."""
+    import transformers as tf
+    from transformers.models.llama.modeling_llama import LlamaAttention as A, LlamaRotaryEmbedding as Rot
+
+    from tritiercache_amd.cache import TriTierCache
+
+    torch.manual_seed(13)
+    cfg = tf.LlamaConfig(hidden_size=1024, num_attention_heads=8, num_key_value_heads=2, head_dim=128,
+                         max_position_embeddings=4096)
+    rot = Rot(config=cfg).to(DEV)
+    layers, caches, lss, logs = [], [], [], []
+    for i in range(2):
+        layer = A(cfg, layer_idx=i).to(DEV).eval()
+        layer.tri_tier_cache = TriTierCache(max_seq_len=1024, head_dim=128, num_heads=2, R_size=64, H_ratio=0.05,
+                                            num_q_heads=8, score_decay=patched.SCORE_DECAY,
+                                            k_group_size=patched.K_GROUP_SIZE,
+                                            pbs_metadata_dtype=patched.PBS_METADATA_DTYPE)
+        c = layer.tri_tier_cache
+        ls = _lockstep_for(oracle, c)
+        log = []
+        prefill, step = c.prefill, c.step_deferred
+
+        def spy_prefill(K, V, prefill=prefill, ls=ls):
+            prefill(K, V)
+            ls.prefill(host(K.float()), host(V.float()))
+
+        def spy_step(Q, K, V, out, prev=None, step=step, log=log):
+            step(Q, K, V, out, prev=prev)
+            log.append((Q.clone(), K.clone(), V.clone(), out, prev))
+
+        c.prefill, c.step_deferred = spy_prefill, spy_step
+        layers.append(layer)
+        caches.append(c)
+        lss.append(ls)
+        logs.append(log)
+    n0 = 400
+    with torch.no_grad():
+        h = torch.randn(1, n0, cfg.hidden_size, device=DEV)
+        pe = rot(h, torch.arange(n0, device=DEV)[None])
+        for layer in layers:
+            layer(h, position_embeddings=pe)
+        for s in range(250):
+            h = torch.randn(1, 1, cfg.hidden_size, device=DEV)
+            pe = rot(h, torch.tensor([[n0 + s]], device=DEV))
+            x = h
+            for layer in layers:
+                x, _ = layer(x, position_embeddings=pe)
+                x = x / x.norm() * 32.0  # keep the next layer's input at a steady scale
+            # layer 1's step ran layer 0's pending feedback in its finalize launch
+            Q0, K0, V0, out0, prev0 = logs[0][-1]
+            Q1, K1, V1, out1, prev1 = logs[1][-1]
+            assert prev1 is caches[0] and (s == 0 or prev0 is caches[1])
+            for i, (Q, K, V, out) in enumerate(((Q0, K0, V0, out0), (Q1, K1, V1, out1))):
+                r = lss[i].step(host(Q), host(K), host(V), host(out), host(caches[i]._engine.get_mean_attn_weights()))
+                assert attention_ok(r), (s, i, r)
+            if (s + 1) % 50 == 0:
+                for i in range(2):
+                    lss[i].check_state(caches[i]._engine, (s, i))
+    for c in caches:
+        assert c.PBS_count > 0 and c.HH_count > 0

@@ -449,6 +449,29 @@ class TriTierCacheEngine:
         _lib.check(_L.tt_engine_step(self._h, q, k, v, o, _stream()), "step")
         st.finish()
 
+    def step_deferred(self, q_ptr, k_ptr, v_ptr, out_ptr, prev=None):
+        """step() for engines stepped one after another (a model's layers): this
+        step runs up to its merged attention output and leaves its mean attention
+        weights and score feedback pending; the pending feedback of `prev`
+        (another TriTierCacheEngine on the same device, or None) runs in this
+        step's finalize launch. A pending feedback also runs at the start of any
+        later call on its engine, or in flush_feedback()."""
+        if prev is self:
+            raise ValueError("prev must be another engine.")
+        st = _Staging()
+        Hq, Hkv, D = self._num_q_heads, self._num_kv_heads, self._head_dim
+        q = st.ptr(q_ptr, "Q", Hq * D * 4)
+        k = st.ptr(k_ptr, "K_new", Hkv * D * 4)
+        v = st.ptr(v_ptr, "V_new", Hkv * D * 4)
+        o = st.ptr(out_ptr, "attn_output", Hq * D * 4, writable=True)
+        ph = prev._h if prev is not None else None
+        _lib.check(_L.tt_engine_step_deferred(self._h, q, k, v, o, ph, _stream()), "step_deferred")
+        st.finish()
+
+    def flush_feedback(self):
+        """Runs this engine's pending mean weights and score feedback, if any."""
+        _lib.check(_L.tt_engine_flush_feedback(self._h, _stream()), "flush_feedback")
+
     def step_with_weights(self, q_ptr, k_ptr, v_ptr, out_ptr) -> torch.Tensor:
         """step() that also returns this step's per-head softmax weights
         [num_q_heads, visible] in the engine's visible order."""

@@ -100,6 +100,19 @@ class TriTierCache:
         [num_q_heads * head_dim]; f32, contiguous, on the engine's device."""
         self._engine.step(Q, K_new, V_new, attn_output)
 
+    def step_deferred(self, Q, K_new, V_new, attn_output, prev=None):
+        """step() for the caches of a model's layers stepped one after another: the
+        context vector is written as by step(), while this step's mean attention
+        weights and score feedback stay pending and run in the finalize launch of
+        the next cache stepped this way (`prev` is the cache stepped just before,
+        on the same device, or None), or at the start of any later call on this
+        cache. The tier state afterwards is the state step() leaves."""
+        self._engine.step_deferred(Q, K_new, V_new, attn_output, None if prev is None else prev._engine)
+
+    def flush_feedback(self):
+        """Runs the pending mean weights and score feedback of the last step_deferred()."""
+        self._engine.flush_feedback()
+
     def step_with_weights(self, Q, K_new, V_new, attn_output):
         """step() plus this step's per-head attention weights [num_q_heads, visible] and the
         token id of each column, ordered as reconstruct_full_cache() orders tokens (sinks,

@@ -17,8 +17,11 @@ unpatched model; then
   vectors; the engine's step (ring ingest, routing, packing, fused attention
   over every tier, score feedback) writes the context vector in device memory,
   which feeds ``o_proj`` directly. No tensor leaves the device and no step
-  synchronises the host. With output_attentions=True the step also returns the
-  per-head weights over the attended tokens.
+  synchronises the host. The layers' steps are chained: each layer's mean
+  attention weights and score feedback run in the next layer's finalize
+  launch (the state afterwards is the state a per-layer step leaves). With
+  output_attentions=True the step also returns the per-head weights over the
+  attended tokens.
 
 There is no path without the engine: a layer whose cache cannot be created
 raises.
@@ -26,6 +29,7 @@ raises.
 from __future__ import annotations
 
 import sys
+import weakref
 from typing import Any, Dict, List, Optional, Tuple, Type
 
 import torch
@@ -69,6 +73,9 @@ def _resolve_families() -> List[Type]:
 
 _SUPPORTED_ATTENTION_CLASSES: List[Type] = _resolve_families()
 _ORIGINAL_FORWARDS: Dict[Type, Any] = {}
+# The cache a decode step last went through, per device: the next layer's step
+# runs that cache's mean weights and score feedback in its own finalize launch.
+_LAST_STEPPED: Dict[int, "weakref.ref"] = {}
 
 
 def _shape(module) -> Tuple[int, int, int]:
@@ -168,7 +175,14 @@ def patched_forward(self, hidden_states: torch.Tensor,
         w, _ = cache.step_with_weights(q_vec, k_vec, v_vec, ctx)
         weights = w.to(hidden_states.dtype).view(1, hq, 1, -1)
     else:
-        cache.step(q_vec, k_vec, v_vec, ctx)
+        # Chained through the model's layers: this layer's mean attention weights
+        # and score feedback run in the next layer's finalize launch (or at this
+        # cache's next call), so a decode step pays one finalize launch per layer.
+        key = hidden_states.device.index if hidden_states.device.index is not None else -1
+        ref = _LAST_STEPPED.get(key)
+        prev = ref() if ref is not None else None
+        cache.step_deferred(q_vec, k_vec, v_vec, ctx, prev=prev if prev is not cache else None)
+        _LAST_STEPPED[key] = weakref.ref(cache)
     return self.o_proj(ctx.view(1, 1, hq * d).to(hidden_states.dtype)), weights
 
 
@@ -191,6 +205,7 @@ def reset_caches(model):
     for module in model.modules():
         if hasattr(module, "tri_tier_cache"):
             delattr(module, "tri_tier_cache")
+    _LAST_STEPPED.clear()
 
 
 def is_patched(model_or_module=None) -> bool:
