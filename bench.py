@@ -57,6 +57,8 @@ CONFIGS = {
     # 256 MB Infinity Cache
     "mha-8k-8layers": (32, 32, 128, 8192, 8, None),
     "qwen2-7b-128k": (28, 4, 128, 131072, 28, "t3"),
+    # head_dim 64 (the SmolLM / TinyLlama / Qwen2-0.5B head size): the VALU split kernel, GQA 4:1
+    "llama-hd64-32k": (32, 8, 64, 32768, 32, "x8"),
 }
 
 
@@ -819,7 +821,7 @@ def main():
         "bytes_read_per_step": bpl * layers,
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_packed_kernel",
+            "kernel": "attn_packed_kernel" if D == 128 or Hkv % 2 == 0 else "attn_split_kernel",
             "achieved": round(kern_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",

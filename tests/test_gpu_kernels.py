@@ -438,15 +438,26 @@ def _tiered_layer(C, Hq, Hkv, D, ctx, fp16, seed, k_outliers=None):
     # more pairs than its logits buffer holds (flushes inside the loop)
     ("llama3-8b-96k", 32, 8, 98304, False, "x8"),
     ("mha-32k", 32, 32, 32768, True, None),
+    # head_dim 64: KV heads taken in pairs as heads of 128 channels on the matrix
+    # cores (GQA 4:1 -> groups of 8, 1:1 -> groups of 2, 7:1 -> 14 in chunks of 8),
+    # and an odd KV head count on the VALU kernel
+    ("hd64-llama-32k", 32, 8, 32768, False, "x8"),
+    ("hd64-llama-32k-fp16", 32, 8, 32768, True, "x8"),
+    ("hd64-mha-8k", 16, 16, 8192, False, None),
+    ("hd64-qwen2-0.5b-32k", 14, 2, 32768, True, "t3"),
+    ("hd64-smollm-8k", 9, 3, 8192, True, None),
 ])
 def test_full_size_layer_vs_oracle(C, oracle, name, Hq, Hkv, ctx, fp16, outliers):
     """A full-context layer against the oracle (the reference's float32 algorithm) and
     against float64 attention over the same exact tier values, elementwise:
     |gpu_i - exact_i| <= 1e-4 |exact_i| + 1e-6 max|exact| for the outputs, relative
     error <= 1e-4 for every mean weight >= 1e-8. Against the float32 oracle the
-    bound is max-normwise 1e-4, and elementwise with 1e-5 max|ref| of absolute
-    slack (the oracle's own sequential float32 sums sit ~1e-6 max|ref| from exact)."""
-    D = 128
+    bound is max-normwise 1e-4 plus the oracle's own normwise distance from the
+    exact result, and elementwise with 1e-5 max|ref| of absolute slack (the
+    oracle's sequential float32 softmax sums sit ~1e-6 max|ref| from exact, and
+    up to ~1e-4 at head_dim 64 with 8x key outliers, where a few keys take most
+    of a head's weight and later terms round away in the running sum)."""
+    D = 64 if name.startswith("hd64") else 128
     Q, dK, dV, nd, blocks, ids, nb = _tiered_layer(C, Hq, Hkv, D, ctx, fp16, seed=ctx + Hkv, k_outliers=outliers)
     out = torch.empty((Hq, D), dtype=torch.float32, device="cuda")
     mw = torch.empty((nd + nb * 16,), dtype=torch.float32, device="cuda")
@@ -461,12 +472,13 @@ def test_full_size_layer_vs_oracle(C, oracle, name, Hq, Hkv, ctx, fp16, outliers
     r = dict(norm_vs_oracle=rel_err(go, ro), elem_vs_oracle=elementwise_ratio(go, ro, atol_frac=1e-5),
              elem_vs_exact=elementwise_ratio(go, xo), mw_norm_vs_oracle=rel_err(gmw, rmw),
              mw_rel_vs_oracle=weights_rel_err(gmw, rmw), mw_rel_vs_exact=weights_rel_err(gmw, xmw),
-             oracle_elem_vs_exact=elementwise_ratio(ro, xo))
+             oracle_elem_vs_exact=elementwise_ratio(ro, xo), oracle_norm_vs_exact=rel_err(ro, xo),
+             oracle_mw_norm_vs_exact=rel_err(rmw, xmw), oracle_mw_rel_vs_exact=weights_rel_err(rmw, xmw))
     print(name, {k: f"{v:.3g}" for k, v in r.items()}, flush=True)
-    assert r["norm_vs_oracle"] <= ATTN_TOL and r["elem_vs_oracle"] <= 1.0, (name, r)
+    assert r["norm_vs_oracle"] <= ATTN_TOL + r["oracle_norm_vs_exact"] and r["elem_vs_oracle"] <= 1.0, (name, r)
     assert r["elem_vs_exact"] <= 1.0, (name, r)
-    assert r["mw_norm_vs_oracle"] <= ATTN_TOL, (name, r)
-    assert r["mw_rel_vs_oracle"] <= 1e-4 and r["mw_rel_vs_exact"] <= 1e-4, (name, r)
+    assert r["mw_norm_vs_oracle"] <= ATTN_TOL + r["oracle_mw_norm_vs_exact"], (name, r)
+    assert r["mw_rel_vs_oracle"] <= 1e-4 + r["oracle_mw_rel_vs_exact"] and r["mw_rel_vs_exact"] <= 1e-4, (name, r)
     assert abs(float(gmw.astype(np.float64).sum()) - 1.0) < 1e-3
 
 

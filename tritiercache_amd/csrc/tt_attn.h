@@ -63,6 +63,10 @@ struct AttnPlan {
     int ld = 0;          // logits row stride (floats)
     int token_ub = 0;    // upper bound on attended tokens
     int dense_delay = 0; // wait of the FP32-tier workgroups before their first load (10 ns ticks)
+    // head_dim 64 with an even KV head count: KV heads 2j and 2j + 1 run as one
+    // head of head_dim 128 on the matrix-core kernel (the plan is that of
+    // num_kv_heads / 2 heads of 128 channels; partials hold 128 channels)
+    bool pair64 = false;
     size_t off_ml = 0, off_acc = 0, off_rowstat = 0, off_logits = 0, bytes = 0;
     bool logits = false;
 };

@@ -404,8 +404,11 @@ __global__ void __launch_bounds__(256) attn_split_kernel(SplitArgs a) {
 //
 // Eight-head groups are held to three waves per SIMD (168 VGPRs, no spills:
 // the loop's rare tail paths and the epilogue recompute their lane indices).
-template <int GP, typename MetaT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(GP == 8 ? 3 : 1)))
+//
+// PAIR: head_dim-64 KV heads 2j and 2j + 1 as one head of 128 channels (the
+// arguments describe num_kv_heads / 2 heads of head_dim 128; see packed_body).
+template <int GP, typename MetaT, bool PAIR = false>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((GP == 8 || PAIR) ? 3 : 1)))
 attn_packed_kernel(SplitArgs a, const int hc, const int chunks) {
     constexpr int kLds = MfLds<GP>::TOTAL > DnLds<GP>::TOTAL ? MfLds<GP>::TOTAL : DnLds<GP>::TOTAL;
     __shared__ __align__(16) char lds[kLds];
@@ -416,10 +419,10 @@ attn_packed_kernel(SplitArgs a, const int hc, const int chunks) {
     if (s >= a.nsplit) return;  // padding slot of the last group of 8
     const int kvh = hz / chunks, chunk = hz - kvh * chunks;
     if (s >= a.nsplit_p) {
-        dense_body<GP>(a, s - a.nsplit_p, kvh, chunk, lds);
+        dense_body<GP, PAIR>(a, s - a.nsplit_p, kvh, chunk, lds);
         return;
     }
-    packed_body<GP, MetaT>(a, s, kvh, chunk, lds);
+    packed_body<GP, MetaT, PAIR>(a, s, kvh, chunk, lds);
 }
 
 // ---------------------------------------------------------------------------
@@ -441,6 +444,7 @@ struct FinArgs {
     int nsplit;
     int D;
     int Hq;
+    int pair_g;  // paired head_dim-64 heads: query heads per real KV head (0: not paired)
     float* out;
     float* rowstat;
     const float* logits;  // null: no mean-weight workgroups
@@ -553,7 +557,13 @@ __device__ __forceinline__ void fin_merge_head(const FinArgs& a, const int h, fl
         const int cq = t >> 2, ci = t & 3;
         float o = 0.0f;
         for (int gg = 0; gg < groups; ++gg) o += red[4 * (gg * q + cq) + ci];
-        a.out[static_cast<size_t>(h) * a.D + t] = (L > 0.0f) ? o / L : 0.0f;
+        o = (L > 0.0f) ? o / L : 0.0f;
+        if (a.pair_g == 0) {
+            a.out[static_cast<size_t>(h) * a.D + t] = o;
+        } else if ((t >> 6) == (h % (2 * a.pair_g)) / a.pair_g) {
+            // a paired head_dim-64 head: its own 64 channels of the pair's 128
+            a.out[static_cast<size_t>(h) * 64 + (t & 63)] = o;
+        }
     }
     if (t == 0) {
         a.rowstat[2 * h] = M;
@@ -998,6 +1008,7 @@ __device__ __forceinline__ FinArgs fin_batch_args(const FinBatchArgs& b, const i
     a.nsplit = b.slot_base[i + 1] - b.slot_base[i];
     a.D = kMfD;
     a.Hq = b.Hq;
+    a.pair_g = 0;
     a.out = d.attn_output;
     a.rowstat = b.rowstat + static_cast<size_t>(i) * 2 * b.Hq;
     a.logits = d.mean_attn_weights ? b.logits + static_cast<size_t>(b.tok_base[i]) * b.Hq : nullptr;
@@ -1052,21 +1063,30 @@ int launch_split_g(const SplitArgs& a, dim3 grid, int gp, int meta_fp16, hipStre
 
 // Grid of attn_packed_kernel: ceil(nsplit / 8) groups of 8 slots for each
 // (KV head, head chunk).
-template <int GP>
+template <int GP, bool PAIR = false>
 int launch_packed_meta(const SplitArgs& a, int Hkv, int chunks, int meta_fp16, hipStream_t st) {
     const int hc = Hkv * chunks;
     const long long wgs = static_cast<long long>((a.nsplit + 7) / 8) * 8 * hc;
     if (wgs > 0x7fffffffLL) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "attention grid too large");
     const dim3 grid(static_cast<unsigned>(wgs));
     if (meta_fp16)
-        hipLaunchKernelGGL((attn_packed_kernel<GP, uint16_t>), grid, dim3(256), 0, st, a, hc, chunks);
+        hipLaunchKernelGGL((attn_packed_kernel<GP, uint16_t, PAIR>), grid, dim3(256), 0, st, a, hc, chunks);
     else
-        hipLaunchKernelGGL((attn_packed_kernel<GP, float>), grid, dim3(256), 0, st, a, hc, chunks);
+        hipLaunchKernelGGL((attn_packed_kernel<GP, float, PAIR>), grid, dim3(256), 0, st, a, hc, chunks);
     TT_LAUNCH_CHECK();
     return TT_OK;
 }
 
-int launch_packed(const SplitArgs& a, int Hkv, int chunks, int gp, int meta_fp16, hipStream_t st) {
+// Paired head_dim-64 heads form groups of 2 G query heads: 2, 4 or 8 per
+// workgroup (G = 1, 2, 4, or 8 and more in chunks of 8).
+int launch_packed(const SplitArgs& a, int Hkv, int chunks, int gp, int meta_fp16, bool pair, hipStream_t st) {
+    if (pair) {
+        switch (gp) {
+        case 2: return launch_packed_meta<2, true>(a, Hkv, chunks, meta_fp16, st);
+        case 4: return launch_packed_meta<4, true>(a, Hkv, chunks, meta_fp16, st);
+        default: return launch_packed_meta<8, true>(a, Hkv, chunks, meta_fp16, st);
+        }
+    }
     switch (gp) {
     case 1: return launch_packed_meta<1>(a, Hkv, chunks, meta_fp16, st);
     case 2: return launch_packed_meta<2>(a, Hkv, chunks, meta_fp16, st);
@@ -1091,7 +1111,14 @@ int gp_for(int G) { return G >= 8 ? 8 : (G > 4 ? 8 : (G > 2 ? 4 : G)); }
 
 
 template <typename MetaT>
-const void* packed_kernel_ptr(int gp) {
+const void* packed_kernel_ptr(int gp, bool pair) {
+    if (pair) {
+        switch (gp) {
+        case 2: return reinterpret_cast<const void*>(&attn_packed_kernel<2, MetaT, true>);
+        case 4: return reinterpret_cast<const void*>(&attn_packed_kernel<4, MetaT, true>);
+        default: return reinterpret_cast<const void*>(&attn_packed_kernel<8, MetaT, true>);
+        }
+    }
     switch (gp) {
     case 1: return reinterpret_cast<const void*>(&attn_packed_kernel<1, MetaT>);
     case 2: return reinterpret_cast<const void*>(&attn_packed_kernel<2, MetaT>);
@@ -1121,13 +1148,13 @@ struct Residency {
     int per_cu = 2;
 };
 
-Residency split_residency(int D, int G, int fp16) {
+Residency split_residency(int D, int G, int fp16, bool pair = false) {
     static std::mutex mu;
-    static std::map<std::tuple<int, int, int, int>, Residency> cache;
+    static std::map<std::tuple<int, int, int, int, int>, Residency> cache;
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return Residency{};
     const int gp = gp_for(G);
-    const auto key = std::make_tuple(dev, D, gp, fp16);
+    const auto key = std::make_tuple(dev, D, gp, fp16, pair ? 1 : 0);
     std::lock_guard<std::mutex> lock(mu);
     auto it = cache.find(key);
     if (it != cache.end()) return it->second;
@@ -1135,7 +1162,7 @@ Residency split_residency(int D, int G, int fp16) {
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
     const void* fn = nullptr;
     if (use_packed_kernel(D)) {
-        fn = fp16 ? packed_kernel_ptr<uint16_t>(gp) : packed_kernel_ptr<float>(gp);
+        fn = fp16 ? packed_kernel_ptr<uint16_t>(gp, pair) : packed_kernel_ptr<float>(gp, pair);
     } else {
         switch (D) {
         case 16: fn = split_kernel_ptr<1>(gp, fp16); break;
@@ -1169,13 +1196,35 @@ int attn_check_shapes(int Hq, int Hkv, int D, int kgs) {
     return TT_OK;
 }
 
+namespace {
+AttnPlan attn_plan_impl(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs, bool need_logits,
+                        int meta_fp16, bool pair);
+}  // namespace
+
+// Head_dim 64 with an even number of KV heads runs as half as many heads of
+// head_dim 128 on the matrix-core kernel: KV heads 2j and 2j + 1 sit next to
+// each other in every tier (K words and scale / zero per block, V words per
+// token, FP32 rows), so they read like one head of 128 channels, and the
+// query heads of both form one group whose queries fill the half of their own
+// head (zeros in the other half), which leaves their logits exact.
 AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs, bool need_logits, int meta_fp16) {
+    if (D == 64 && Hkv % 2 == 0) {
+        AttnPlan p = attn_plan_impl(dense_ub, blocks_ub, Hq, Hkv / 2, kMfD, kgs, need_logits, meta_fp16, true);
+        p.pair64 = true;
+        return p;
+    }
+    return attn_plan_impl(dense_ub, blocks_ub, Hq, Hkv, D, kgs, need_logits, meta_fp16, false);
+}
+
+namespace {
+AttnPlan attn_plan_impl(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs, bool need_logits,
+                        int meta_fp16, bool pair) {
     AttnPlan p;
     const int W = kgs / 16;
     const int G = Hq / Hkv;
     const int chunks = (G + gp_for(G) - 1) / gp_for(G);
     const long long heads = static_cast<long long>(Hkv) * chunks;
-    const Residency res = split_residency(D, G, meta_fp16);
+    const Residency res = split_residency(D, G, meta_fp16, pair);
     const long long resident = static_cast<long long>(res.cus) * res.per_cu;
     const long long per_head = std::max<long long>(1, (resident + heads - 1) / heads);
     const long long dense_tiles = (dense_ub + 15) / 16;
@@ -1251,14 +1300,21 @@ AttnPlan attn_plan(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int kgs,
     p.bytes = off;
     return p;
 }
+}  // namespace
 
-int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipStream_t stream) {
-    if (plan.logits && !logits_fit(in.Hq, plan.ld))
+int attn_launch_split(const AttnInputs& real_in, const AttnPlan& plan, void* ws, hipStream_t stream) {
+    if (plan.logits && !logits_fit(real_in.Hq, plan.ld))
         TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_q_heads x tokens exceeds the 4 GiB logits buffer of the mean weights.");
+    // paired head_dim-64 heads: the kernel sees half as many heads of 128 channels
+    AttnInputs in = real_in;
+    if (plan.pair64) {
+        in.D = kMfD;
+        in.Hkv = real_in.Hkv / 2;
+    }
     char* base = static_cast<char*>(ws);
     SplitArgs a;
     a.in = in;
-    a.scale2 = kLog2e / sqrtf(static_cast<float>(in.D));
+    a.scale2 = kLog2e / sqrtf(static_cast<float>(real_in.D));
     a.part_ml = reinterpret_cast<float*>(base + plan.off_ml);
     a.part_acc = reinterpret_cast<float*>(base + plan.off_acc);
     a.logits = plan.logits ? reinterpret_cast<float*>(base + plan.off_logits) : nullptr;
@@ -1274,7 +1330,7 @@ int attn_launch_split(const AttnInputs& in, const AttnPlan& plan, void* ws, hipS
     const int chunks = (G + gp - 1) / gp;
     if (use_packed_kernel(in.D)) {
         if (plan.nsplit_p <= 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
-        return launch_packed(a, in.Hkv, chunks, gp, in.meta_fp16, stream);
+        return launch_packed(a, in.Hkv, chunks, gp, in.meta_fp16, plan.pair64, stream);
     }
     const dim3 grid(plan.nsplit, in.Hkv, chunks);
     if (plan.nsplit_p != 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
@@ -1295,7 +1351,8 @@ FinArgs fin_args(const AttnInputs& in, const AttnPlan& plan, void* ws, float* ou
     f.part_ml = reinterpret_cast<const float*>(base + plan.off_ml);
     f.part_acc = reinterpret_cast<const float*>(base + plan.off_acc);
     f.nsplit = plan.nsplit;
-    f.D = in.D;
+    f.D = plan.pair64 ? kMfD : in.D;
+    f.pair_g = plan.pair64 ? in.Hq / in.Hkv : 0;
     f.Hq = in.Hq;
     f.out = out;
     f.rowstat = reinterpret_cast<float*>(base + plan.off_rowstat);

@@ -69,10 +69,10 @@ struct MfLds {
     static constexpr int KT = 0;       // [2 tiles][4 token quads][kKTS dwords]
     static constexpr int VT = 1152;    // [32 byte columns][8 dwords] + 1 (vt_dword), token bytes in MFMA order
     static constexpr int KSZ = 2432;   // [2 tiles][scale | zero][kKSZ] f32
-    static constexpr int VS = 4736;    // [32] f32, MFMA token order (0 for masked slots)
-    static constexpr int VZ = 4864;    // [32] f32
-    static constexpr int BIAS = 4992;  // [2 tiles][8] f32 per-head QK bias
-    static constexpr int BHL = 5056;   // [NBT tiles][hi rows 0..GP-1, lo rows GP..2GP-1][kBRS] f16
+    static constexpr int VS = 4736;    // [2 halves][32] f32, MFMA token order (0 for masked slots); half 1: paired heads
+    static constexpr int VZ = 4992;    // [2][32] f32
+    static constexpr int BIAS = 5248;  // [2 tiles][8] f32 per-head QK bias
+    static constexpr int BHL = 5312;   // [NBT tiles][hi rows 0..GP-1, lo rows GP..2GP-1][kBRS] f16
     static constexpr int BHL_TILE = 2 * GP * kBRS * 2;
     // Coefficient tiles held at once. Eight heads keep one (the second tile
     // of a pair reuses it), which brings the workgroup under a third of the
@@ -249,6 +249,10 @@ struct MetaRaw<float> {
     __device__ __forceinline__ static One load1(const float* p) { return *p; }
     __device__ __forceinline__ static float4 f4(const Four v) { return v; }
     __device__ __forceinline__ static float f1(const One v) { return v; }
+    // two adjacent values (the V scale or zero of a pair of head_dim-64 heads)
+    using Two = float2;
+    __device__ __forceinline__ static Two load2(const float* p) { return *reinterpret_cast<const float2*>(p); }
+    __device__ __forceinline__ static float2 f2(const Two v) { return v; }
 };
 template <>
 struct MetaRaw<uint16_t> {
@@ -265,6 +269,11 @@ struct MetaRaw<uint16_t> {
                            f16_to_f32(static_cast<uint16_t>(v.y & 0xffffu)), f16_to_f32(static_cast<uint16_t>(v.y >> 16)));
     }
     __device__ __forceinline__ static float f1(const One v) { return f16_to_f32(static_cast<uint16_t>(v)); }
+    using Two = uint32_t;
+    __device__ __forceinline__ static Two load2(const uint16_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+    __device__ __forceinline__ static float2 f2(const Two v) {
+        return make_float2(f16_to_f32(static_cast<uint16_t>(v & 0xffffu)), f16_to_f32(static_cast<uint16_t>(v >> 16)));
+    }
 };
 
 // Stores that write through the L2 (device scope): the partials and logits
@@ -304,14 +313,26 @@ __device__ __forceinline__ void dense_range(const SplitArgs& a, const int Nd, co
 // The group's query heads into LDS ([GP][128] f32, heads past gc as zeros).
 // Issued before any other global load of the workgroup: loads return in
 // order, so the barrier that follows then waits for this load only.
-template <int GP>
+// PAIR (head_dim-64 heads 2j, 2j + 1 as one head of 128 channels): the query
+// of the group's head g has 64 channels and fills the half of its own KV head,
+// (g0 + g) / (G / 2), with zeros in the other half, so its logits are those of
+// its own head.
+template <int GP, bool PAIR = false>
 __device__ __forceinline__ void load_q_lds(const AttnInputs& in, const int kvh, const int g0, const int gc,
                                            float* q_l) {
     const int G = in.Hq / in.Hkv;
     for (int idx = threadIdx.x; idx < GP * (kMfD / 4); idx += 256) {
         const int g = idx / (kMfD / 4), c4 = idx - g * (kMfD / 4);
         float4 v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (g < gc) v = *reinterpret_cast<const float4*>(in.Q + static_cast<size_t>(kvh * G + g0 + g) * kMfD + 4 * c4);
+        if (g < gc) {
+            const size_t row = static_cast<size_t>(kvh * G + g0 + g);
+            if constexpr (PAIR) {
+                if ((c4 >> 4) == (g0 + g) / (G >> 1))
+                    v = *reinterpret_cast<const float4*>(in.Q + row * (kMfD / 2) + 4 * (c4 & 15));
+            } else {
+                v = *reinterpret_cast<const float4*>(in.Q + row * kMfD + 4 * c4);
+            }
+        }
         *reinterpret_cast<float4*>(q_l + g * kMfD + 4 * c4) = v;
     }
 }
@@ -520,7 +541,7 @@ __device__ __forceinline__ void dense_share(const SplitArgs& a, const DenseView&
 // One FP32-tier workgroup: KV head kvh, query heads [GP * chunk, +GP), FP32
 // tiles [d0, d1) of share `dsplit`. The four waves' partials merge in LDS
 // into partial slot nsplit_p + dsplit of each head.
-template <int GP>
+template <int GP, bool PAIR = false>
 __device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit, const int kvh, const int chunk,
                                            char* lds) {
     using L = DnLds<GP>;
@@ -534,7 +555,7 @@ __device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit,
     dense_range(a, dv.Nd, dsplit, d0, d1);
     float* q_l = reinterpret_cast<float*>(lds + L::QL);
     float* dl = reinterpret_cast<float*>(lds + L::PART);
-    load_q_lds<16>(in, kvh, g0, gc, q_l);  // rows past the group's heads are zeros
+    load_q_lds<16, PAIR>(in, kvh, g0, gc, q_l);  // rows past the group's heads are zeros
     if (a.dense_delay > 0) {
         // bounded by the constant-rate real-time counter
         const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
@@ -587,7 +608,7 @@ __device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit,
 // leaves every column the logits of its own tile, and each lane runs the
 // softmax over 4 tokens rather than 8. In the PV operand the K elements
 // of the other tile are zero, which keeps the token order of the V codes.
-template <int GP, typename MetaT>
+template <int GP, typename MetaT, bool PAIR = false>
 __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split, const int kvh, const int chunk,
                                             char* lds) {
     static_assert(GP >= 1 && GP <= 8, "at most 8 query heads per workgroup");
@@ -639,13 +660,15 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     // The query heads first (the barrier below waits for them only), then the
     // wave's first pair of packed tiles, whose latency overlaps theirs.
     float* q_l = reinterpret_cast<float*>(lds + L::QL);
-    load_q_lds<GP>(in, kvh, g0, gc, q_l);
+    load_q_lds<GP, PAIR>(in, kvh, g0, gc, q_l);
     const int32_t* kp_h = in.kp + kvh * kMfD;
     const MetaT* ks_h = static_cast<const MetaT*>(in.ks) + kvh * kMfD;
     const MetaT* kz_h = static_cast<const MetaT*>(in.kz) + kvh * kMfD;
     const int32_t* vp_h = in.vp + kvh * (kMfD / 16);
-    const MetaT* vs_h = static_cast<const MetaT*>(in.vs) + kvh;
-    const MetaT* vz_h = static_cast<const MetaT*>(in.vz) + kvh;
+    // V scale / zero per (token, KV head); paired heads: the two of the pair, adjacent
+    const int hkv_m = PAIR ? 2 * Hkv : Hkv;
+    const MetaT* vs_h = static_cast<const MetaT*>(in.vs) + (PAIR ? 2 * kvh : kvh);
+    const MetaT* vz_h = static_cast<const MetaT*>(in.vz) + (PAIR ? 2 * kvh : kvh);
     const int lk = 4 * (lane & 31);
     const int tv = 4 * (lane >> 3) + (lane & 3);
     const int hfo = 4 * ((lane >> 2) & 1);
@@ -664,7 +687,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         return PairOffs{static_cast<uint32_t>(kto * tstride + lk) * 4u,
                         static_cast<uint32_t>(((W == 2) ? 0 : kto) * tstride + lk) * static_cast<uint32_t>(sizeof(MetaT)),
                         static_cast<uint32_t>(min(tv, lim) * vstride + hfo) * 4u,
-                        static_cast<uint32_t>(ts * Hkv) * static_cast<uint32_t>(sizeof(MetaT)),
+                        static_cast<uint32_t>(ts * hkv_m) * static_cast<uint32_t>(sizeof(MetaT)),
                         static_cast<uint32_t>(ts) * 8u};
     };
     const PairOffs off_full = pair_offs(lane >> 5, 31);
@@ -676,6 +699,7 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     mf_u4 kw, vw;
     typename MR::Four ksr, kzr;
     typename MR::One vm = 0;
+    typename MR::Two vm2{};
     long long idv = -1;
     bool okv = false;
 
@@ -690,10 +714,17 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         kzr = MR::load4(reinterpret_cast<const MetaT*>(at(kz_h + mb, o.km)));
         vw = *reinterpret_cast<const mf_u4*>(at(vp_h + s0 * vstride, o.v));
         // V scale in lanes 0-31, V zero in lanes 32-63 (two half-wave loads)
-        if (lane < 32)
-            vm = MR::load1(reinterpret_cast<const MetaT*>(at(vs_h + s0 * Hkv, o.vm)));
-        else
-            vm = MR::load1(reinterpret_cast<const MetaT*>(at(vz_h + s0 * Hkv, o.vm)));
+        if constexpr (PAIR) {
+            if (lane < 32)
+                vm2 = MR::load2(reinterpret_cast<const MetaT*>(at(vs_h + s0 * hkv_m, o.vm)));
+            else
+                vm2 = MR::load2(reinterpret_cast<const MetaT*>(at(vz_h + s0 * hkv_m, o.vm)));
+        } else {
+            if (lane < 32)
+                vm = MR::load1(reinterpret_cast<const MetaT*>(at(vs_h + s0 * Hkv, o.vm)));
+            else
+                vm = MR::load1(reinterpret_cast<const MetaT*>(at(vz_h + s0 * Hkv, o.vm)));
+        }
         idv = *reinterpret_cast<const long long*>(at(in.ids + s0, o.id));
     };
     auto fetch = [&](const int p) {
@@ -757,8 +788,12 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
     const uint32_t kmask = (3u << (2 * (lane & 3))) | (3u << (16 + 2 * (lane & 3)));
     uint32_t one024;
     asm volatile("v_mov_b32 %0, 0x64006400" : "=v"(one024));
-    const uint32_t qsel1 = (lane & 1) ? 0x03070105u : 0x06020400u;
-    const uint32_t qsel2 = (lane & 2) ? 0x03020706u : 0x05040100u;
+    // byte selectors of the V transpose (paired eight-head groups recompute
+    // them in the lay-out from an opaque copy of the thread id: held over the
+    // loop they would push that kernel past 168 VGPRs)
+    constexpr bool kLeanSel = PAIR && GP == 8;
+    const uint32_t qsel1_c = (lane & 1) ? 0x03070105u : 0x06020400u;
+    const uint32_t qsel2_c = (lane & 2) ? 0x03020706u : 0x05040100u;
 
     mf_f4 acc[8];
 #pragma unroll
@@ -781,6 +816,13 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         const int m = lane >> 3;
         const int hf = (lane >> 2) & 1;
         const uint32_t vwv[4] = {vw.x, vw.y, vw.z, vw.w};
+        uint32_t qsel1 = qsel1_c, qsel2 = qsel2_c;
+        if constexpr (kLeanSel) {
+            int tx = static_cast<int>(threadIdx.x);
+            asm volatile("" : "+v"(tx));
+            qsel1 = (tx & 1) ? 0x03070105u : 0x06020400u;
+            qsel2 = (tx & 2) ? 0x03020706u : 0x05040100u;
+        }
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const uint32_t x = vwv[g];
@@ -796,10 +838,22 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         const int pos = 8 * ((t2 & 15) >> 2) + 4 * (t2 >> 4) + (t2 & 3);
         // lanes 32-63 hold the token's zero, lanes 0-31 its scale: the zero of
         // the centred codes is vz + 1.5 vs (the middle of the row's range)
-        const float mv = MR::f1(vm);
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mv), __float_as_uint(mv), false, false);
-        const float mc = lane < 32 ? mv : __builtin_fmaf(1.5f, __uint_as_float(sw[0]), mv);
-        (lane < 32 ? vs_l : vz_l)[pos] = ok ? mc : 0.0f;  // masked slots contribute nothing
+        if constexpr (PAIR) {
+            // both heads of the pair: half 0 at [0, 32), half 1 at [32, 64)
+            const float2 mv = MR::f2(vm2);
+            const auto sx = __builtin_amdgcn_permlane32_swap(__float_as_uint(mv.x), __float_as_uint(mv.x), false, false);
+            const auto sy = __builtin_amdgcn_permlane32_swap(__float_as_uint(mv.y), __float_as_uint(mv.y), false, false);
+            const float mx = lane < 32 ? mv.x : __builtin_fmaf(1.5f, __uint_as_float(sx[0]), mv.x);
+            const float my = lane < 32 ? mv.y : __builtin_fmaf(1.5f, __uint_as_float(sy[0]), mv.y);
+            float* dst = lane < 32 ? vs_l : vz_l;
+            dst[pos] = ok ? mx : 0.0f;  // masked slots contribute nothing
+            dst[32 + pos] = ok ? my : 0.0f;
+        } else {
+            const float mv = MR::f1(vm);
+            const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mv), __float_as_uint(mv), false, false);
+            const float mc = lane < 32 ? mv : __builtin_fmaf(1.5f, __uint_as_float(sw[0]), mv);
+            (lane < 32 ? vs_l : vz_l)[pos] = ok ? mc : 0.0f;  // masked slots contribute nothing
+        }
         return static_cast<uint32_t>(__ballot(ok));
     };
 
@@ -908,10 +962,12 @@ __device__ __forceinline__ void packed_body(const SplitArgs& a, const int split,
         float vsv[NT][4], vzv[NT][4];
         uint2 q0, q1;
         auto read_v = [&]() {
+            // paired heads: the V scale / zero of the column's own head
+            const int vh = PAIR ? 32 * min(1, (g0 + bhead) / (G >> 1)) : 0;
 #pragma unroll
             for (int i = 0; i < NT; ++i) {
-                const float4 vq = *reinterpret_cast<const float4*>(vs_l + 8 * gk + 4 * tt(i));
-                const float4 zq = *reinterpret_cast<const float4*>(vz_l + 8 * gk + 4 * tt(i));
+                const float4 vq = *reinterpret_cast<const float4*>(vs_l + vh + 8 * gk + 4 * tt(i));
+                const float4 zq = *reinterpret_cast<const float4*>(vz_l + vh + 8 * gk + 4 * tt(i));
                 vsv[i][0] = vq.x; vsv[i][1] = vq.y; vsv[i][2] = vq.z; vsv[i][3] = vq.w;
                 vzv[i][0] = zq.x; vzv[i][1] = zq.y; vzv[i][2] = zq.z; vzv[i][3] = zq.w;
             }
