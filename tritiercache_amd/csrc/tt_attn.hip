@@ -427,10 +427,11 @@ attn_packed_kernel(SplitArgs a, const int hc, const int chunks) {
 
 // ---------------------------------------------------------------------------
 // Finalize: one launch with two kinds of workgroups.
-//   [0, Hq)        merge the split partials of query head h (log2 units):
+//   [0, Hq S)      merge the split partials of query head h (log2 units),
+//                  S workgroups per head, one per 32 output channels:
 //                  M = max_j m_j, L = sum_j l_j 2^(m_j - M),
 //                  out = sum_j acc_j 2^(m_j - M) / L.
-//   [Hq, ...)      mean attention weights of blocks of kMeanTokens (long contexts: kMeanTokensLong) tokens
+//   [Hq S, ...)    mean attention weights of blocks of kMeanTokens (long contexts: kMeanTokensLong) tokens
 //                  (fused_attn_avx2.cpp:286-300): every such workgroup first
 //                  rebuilds (M, 1/L) of all heads from the (m, l) partials,
 //                  then w_h = 2^(s_h - M_h) / L_h summed over the heads and
@@ -492,14 +493,30 @@ __device__ __forceinline__ float4 load_ml_pair(const float* p) {
     return make_float4(a.x, a.y, b.x, b.y);
 }
 
-__device__ __forceinline__ void fin_merge_head(const FinArgs& a, const int h, float* sh) {
+// Workgroups per query head in the merge. One workgroup holds the loads of
+// kMergeU splits per thread-group in flight (16384 / width splits for `width`
+// channels); a head with more splits than that is cut into slices of 32
+// channels (head_dim a multiple of 32), each merged by its own workgroup that
+// rebuilds the head's (M, L) from the split statistics, so the merge stays
+// one round trip of loads. A paired head_dim-64 head covers only its own 64
+// channels of the pair's 128.
+__host__ __device__ inline int fin_merge_slices(const int D, const int pair_g, const int nsplit) {
+    const int need = pair_g ? 64 : D;
+    if (nsplit * need <= 16 * 256 * 4 || need % 32 != 0) return 1;
+    return need / 32;
+}
+
+__device__ __forceinline__ void fin_merge_head(const FinArgs& a, const int h, const int slice, const int msl,
+                                               float* sh) {
     const int t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const float* ml = a.part_ml + static_cast<size_t>(h) * a.nsplit * 2;
-    const int q = a.D >> 2;
+    const int width = (a.pair_g ? 64 : a.D) / msl;
+    const int c0 = (a.pair_g ? ((h % (2 * a.pair_g)) / a.pair_g) * 64 : 0) + width * slice;
+    const int q = width >> 2;
     const int groups = 256 / q;
     const int g = t / q, c4 = t - g * q;
-    const float* base = a.part_acc + static_cast<size_t>(h) * a.nsplit * a.D + 4 * c4;
+    const float* base = a.part_acc + static_cast<size_t>(h) * a.nsplit * a.D + c0 + 4 * c4;
     float* red = sh + 8;  // [256][4]
     float4 A = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     float L = 0.0f, M = kNegInf;
@@ -553,19 +570,17 @@ __device__ __forceinline__ void fin_merge_head(const FinArgs& a, const int h, fl
     }
     *reinterpret_cast<float4*>(red + 4 * t) = A;
     __syncthreads();
-    if (t < a.D) {
+    if (t < width) {
         const int cq = t >> 2, ci = t & 3;
         float o = 0.0f;
         for (int gg = 0; gg < groups; ++gg) o += red[4 * (gg * q + cq) + ci];
         o = (L > 0.0f) ? o / L : 0.0f;
-        if (a.pair_g == 0) {
-            a.out[static_cast<size_t>(h) * a.D + t] = o;
-        } else if ((t >> 6) == (h % (2 * a.pair_g)) / a.pair_g) {
-            // a paired head_dim-64 head: its own 64 channels of the pair's 128
-            a.out[static_cast<size_t>(h) * 64 + (t & 63)] = o;
-        }
+        if (a.pair_g == 0)
+            a.out[static_cast<size_t>(h) * a.D + c0 + t] = o;
+        else  // a paired head_dim-64 head: its own 64 channels of the pair's 128
+            a.out[static_cast<size_t>(h) * 64 + (c0 & 63) + t] = o;
     }
-    if (t == 0) {
+    if (t == 0 && slice == 0) {
         a.rowstat[2 * h] = M;
         a.rowstat[2 * h + 1] = L;
     }
@@ -716,8 +731,17 @@ __device__ __forceinline__ void fin_mean_tokens(const FinArgs& a, const int wg, 
     constexpr int kU4 = 8;
     bool logits_issued = false;
     if (kRowstat) {
-        // published by the merge (attn_finalize_kernel's merge role)
-        for (int h = t; h < Hq; h += 256) {
+        // Published by the merge (attn_finalize_kernel's merge role). The
+        // first 256 heads' statistics and the first block's logits are in
+        // flight together; storing the statistics waits for them alone.
+        const float2 r0 = *reinterpret_cast<const float2*>(a.rowstat + 2 * (t < Hq ? t : Hq - 1));
+        fin_load_logits_nb<MT, NU>(a, hg, wg * MT + 4 * q, n, lgv);
+        logits_issued = true;
+        if (t < Hq) {
+            Mh[t] = r0.x;
+            iL[t] = 1.0f / (r0.y > 0.0f ? r0.y : 1.0f);
+        }
+        for (int h = t + 256; h < Hq; h += 256) {
             const float2 r = *reinterpret_cast<const float2*>(a.rowstat + 2 * h);
             Mh[h] = r.x;
             iL[h] = 1.0f / (r.y > 0.0f ? r.y : 1.0f);
@@ -876,13 +900,15 @@ template <int MT>
 __global__ void __launch_bounds__(256) attn_finalize_kernel(FinArgs a) {
     extern __shared__ float sh[];
     const int b = static_cast<int>(blockIdx.x);
-    if (b < a.Hq)
-        fin_merge_head(a, b, sh);
+    const int msl = fin_merge_slices(a.D, a.pair_g, a.nsplit);
+    const int merges = a.Hq * msl;
+    if (b < merges)
+        fin_merge_head(a, b / msl, b % msl, msl, sh);
     else
-        fin_mean_dispatch<MT, false>(a, b - a.Hq, static_cast<int>(gridDim.x) - a.Hq, sh);
+        fin_mean_dispatch<MT, false>(a, b - merges, static_cast<int>(gridDim.x) - merges, sh);
 }
 
-// The merge of one call's partials (workgroups [0, Hq)) beside the mean
+// The merge of one call's partials (workgroups [0, Hq S)) beside the mean
 // weights of an earlier merge-only call whose partials, logits and row
 // statistics sit in another workspace: a caller that runs layers back to back
 // folds each layer's mean weights into the next layer's finalize launch.
@@ -890,10 +916,12 @@ template <int MT>
 __global__ void __launch_bounds__(256) attn_finalize_deferred_kernel(FinArgs am, FinArgs aw) {
     extern __shared__ float sh[];
     const int b = static_cast<int>(blockIdx.x);
-    if (b < am.Hq)
-        fin_merge_head(am, b, sh);
+    const int msl = fin_merge_slices(am.D, am.pair_g, am.nsplit);
+    const int merges = am.Hq * msl;
+    if (b < merges)
+        fin_merge_head(am, b / msl, b % msl, msl, sh);
     else
-        fin_mean_dispatch<MT, true>(aw, b - am.Hq, static_cast<int>(gridDim.x) - am.Hq, sh);
+        fin_mean_dispatch<MT, true>(aw, b - merges, static_cast<int>(gridDim.x) - merges, sh);
 }
 
 // The mean-weight role alone, after a merge-only finalize of the same
@@ -995,6 +1023,7 @@ struct FinBatchArgs {
     const float* logits;
     float* rowstat;
     int nseq, Hq, kgs;
+    int msl;  // merge workgroups per (sequence, query head)
     int slot_base[kMaxBatchSeqs + 1];
     int tok_base[kMaxBatchSeqs + 1];
     int mean_base[kMaxBatchSeqs + 1];
@@ -1023,16 +1052,19 @@ __device__ __forceinline__ FinArgs fin_batch_args(const FinBatchArgs& b, const i
     return a;
 }
 
-// Workgroups [0, nseq Hq): the merge of (sequence, query head); the rest:
+// Workgroups [0, nseq Hq S): the merge of (sequence, query head, channel
+// slice); the rest:
 // mean weights, sequence i owning [mean_base[i], mean_base[i + 1]).
 __global__ void __launch_bounds__(256) attn_finalize_batched_kernel(const FinBatchArgs b) {
     extern __shared__ float sh[];
     const int blk = static_cast<int>(blockIdx.x);
-    const int merges = b.nseq * b.Hq;
+    const int msl = b.msl;
+    const int merges = b.nseq * b.Hq * msl;
     if (blk < merges) {
-        const int i = blk / b.Hq;
+        const int i = blk / (b.Hq * msl);
         const FinArgs a = fin_batch_args(b, i);
-        fin_merge_head(a, blk - i * b.Hq, sh);
+        const int r = blk - i * b.Hq * msl;
+        fin_merge_head(a, r / msl, r % msl, msl, sh);
         return;
     }
     const int m = blk - merges;
@@ -1394,6 +1426,7 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
     const int mt = fin_mean_tokens_per_block(plan);
     const int mean_wgs = fin_mean_wgs(plan, weights && roles != FinRoles::kMerge);
     const size_t lds = fin_lds_bytes(in.Hq);
+    const int merges = in.Hq * fin_merge_slices(f.D, f.pair_g, f.nsplit);
     if (roles == FinRoles::kMean) {
         if (mean_wgs == 0) return TT_OK;
         if (mt == kMeanTokensLong)
@@ -1401,9 +1434,9 @@ int attn_launch_finalize(const AttnInputs& in, const AttnPlan& plan, void* ws, f
         else
             hipLaunchKernelGGL(attn_mean_kernel<kMeanTokens>, dim3(mean_wgs), dim3(256), lds, stream, f);
     } else if (mt == kMeanTokensLong) {
-        hipLaunchKernelGGL(attn_finalize_kernel<kMeanTokensLong>, dim3(in.Hq + mean_wgs), dim3(256), lds, stream, f);
+        hipLaunchKernelGGL(attn_finalize_kernel<kMeanTokensLong>, dim3(merges + mean_wgs), dim3(256), lds, stream, f);
     } else {
-        hipLaunchKernelGGL(attn_finalize_kernel<kMeanTokens>, dim3(in.Hq + mean_wgs), dim3(256), lds, stream, f);
+        hipLaunchKernelGGL(attn_finalize_kernel<kMeanTokens>, dim3(merges + mean_wgs), dim3(256), lds, stream, f);
     }
     TT_LAUNCH_CHECK();
     return TT_OK;
@@ -1417,12 +1450,13 @@ int attn_launch_finalize_deferred(const AttnInputs& in, const AttnPlan& plan, vo
     if (!aw.logits) TT_FAIL(TT_ERR_RUNTIME, "deferred mean weights without logits in the earlier workspace");
     const int mean_wgs = fin_mean_wgs(prev_plan, true);
     const size_t lds = std::max(fin_lds_bytes(in.Hq), fin_lds_bytes(prev_in.Hq));
+    const int merges = in.Hq * fin_merge_slices(am.D, am.pair_g, am.nsplit);
     if (fin_mean_tokens_per_block(prev_plan) == kMeanTokensLong)
-        hipLaunchKernelGGL(attn_finalize_deferred_kernel<kMeanTokensLong>, dim3(in.Hq + mean_wgs), dim3(256), lds,
+        hipLaunchKernelGGL(attn_finalize_deferred_kernel<kMeanTokensLong>, dim3(merges + mean_wgs), dim3(256), lds,
                            stream, am, aw);
     else
-        hipLaunchKernelGGL(attn_finalize_deferred_kernel<kMeanTokens>, dim3(in.Hq + mean_wgs), dim3(256), lds, stream,
-                           am, aw);
+        hipLaunchKernelGGL(attn_finalize_deferred_kernel<kMeanTokens>, dim3(merges + mean_wgs), dim3(256), lds,
+                           stream, am, aw);
     TT_LAUNCH_CHECK();
     return TT_OK;
 }
@@ -1540,11 +1574,14 @@ int batch_launch(const BatchPlan& plan, const tt_decode_seq* seqs_dev, int Hq, i
     f.nseq = plan.nseq;
     f.Hq = Hq;
     f.kgs = kgs;
+    int max_split = 1;
+    for (int i = 0; i < plan.nseq; ++i) max_split = std::max(max_split, plan.slot_base[i + 1] - plan.slot_base[i]);
+    f.msl = fin_merge_slices(kMfD, 0, max_split);
     std::memcpy(f.slot_base, plan.slot_base, sizeof(f.slot_base));
     std::memcpy(f.tok_base, plan.tok_base, sizeof(f.tok_base));
     std::memcpy(f.mean_base, plan.mean_base, sizeof(f.mean_base));
     const size_t lds = sizeof(float) * std::max<size_t>(8 + 4 * 256, 2 * static_cast<size_t>(Hq) + 256 * 4);
-    const long long fwgs = static_cast<long long>(plan.nseq) * Hq + plan.mean_base[plan.nseq];
+    const long long fwgs = static_cast<long long>(plan.nseq) * Hq * f.msl + plan.mean_base[plan.nseq];
     hipLaunchKernelGGL(attn_finalize_batched_kernel, dim3(static_cast<unsigned>(fwgs)), dim3(256), lds, stream, f);
     TT_LAUNCH_CHECK();
     return TT_OK;
