@@ -91,7 +91,7 @@ TT_API int tt_dequantize_v(const int32_t* packed, const void* scale, const void*
  * -1 token ids masked, optional mean attention weights
  * [dense_count + num_blocks*k_group_size].
  * Requirements beyond the reference's: num_q_heads % num_kv_heads == 0,
- * head_dim one of 16, 32, 64, 128, 256, and, with mean weights,
+ * head_dim a multiple of 16 of at most 256, and, with mean weights,
  * num_q_heads x tokens x 4 bytes of logits within 4 GiB (the same bound
  * holds for every attention entry point and for tt_engine_create's
  * max_seq_len).

@@ -29,6 +29,12 @@ RUNS = {
     # long prefill: thresholds over ~36k candidates (the many-workgroup selection on the GPU)
     "step_long_prefill_fp32": dict(mode="step", Hq=4, Hkv=1, D=64, msl=36200, S=4, R=32, hr=0.05, decay=0.999,
                                    iv=32, kgs=16, fp16=False, steps=70, prefill=36000, seed=14, every=32),
+    # head_dims that are multiples of 16 but not powers of two (the VALU kernel with
+    # lane channel ranges straddling V words; the flush's V rows on padded lane groups)
+    "step_d80_fp16": dict(mode="step", Hq=6, Hkv=2, D=80, msl=1024, S=4, R=16, hr=0.1, decay=0.999, iv=16,
+                          kgs=16, fp16=True, steps=200, prefill=64, seed=17, every=40),
+    "step_d96_kgs32_fp32": dict(mode="step", Hq=12, Hkv=4, D=96, msl=1024, S=4, R=16, hr=0.1, decay=0.999,
+                                iv=32, kgs=32, fp16=False, steps=200, prefill=40, seed=18, every=40),
     "inject_maint_fp16": dict(mode="inject", Hq=32, Hkv=32, D=128, msl=2048, S=4, R=256, hr=0.05, decay=0.999,
                               iv=32, kgs=16, fp16=True, steps=2048, prefill=0, seed=2, every=128),
     "inject_maint_fp32": dict(mode="inject", Hq=32, Hkv=32, D=128, msl=2048, S=4, R=256, hr=0.05, decay=0.999,

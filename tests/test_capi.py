@@ -177,13 +177,15 @@ def test_workspace_size_query_validates_like_the_entry_points():
     L = _lib.load()
     q = L.tt_fused_attention_workspace_bytes
     for args, msg in [((-1, 5, 32, 8, 128, 16, 1), "dense_count"), ((10, -2, 32, 8, 128, 16, 1), "num_blocks"),
-                      ((10, 5, 32, 7, 128, 16, 1), "multiple"), ((10, 5, 32, 8, 96, 16, 1), "head_dim"),
+                      ((10, 5, 32, 7, 128, 16, 1), "multiple"), ((10, 5, 32, 8, 72, 16, 1), "head_dim"),
+                      ((10, 5, 32, 8, 272, 16, 1), "head_dim"),
                       ((10, 5, 32, 8, 128, 24, 1), "k_group_size"),
                       ((1 << 30, 1 << 26, 64, 8, 128, 32, 1), "2^31"),
                       ((1 << 28, 0, 64, 8, 128, 16, 1), "4 GiB")]:
         assert q(*args) == 0 and msg in _lib.last_error(), (args, _lib.last_error())
     assert q(1 << 28, 0, 64, 8, 128, 16, 0) > 0  # no mean weights: no logits
     assert q(300, 120, 32, 8, 128, 16, 1) > 0 and _lib.last_error() == ""
+    assert q(300, 120, 32, 8, 96, 16, 1) > 0 and _lib.last_error() == ""  # any multiple of 16 up to 256
     # the entry points reject the same token count
     p = 0x10000
     rc = L.tt_attention_partials(p, p, p, 1 << 30, p, p, p, p, p, p, p, 1 << 26, 64, 8, 128, 32, 0, 0, p, 1 << 40, None)

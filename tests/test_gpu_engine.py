@@ -60,7 +60,8 @@ def _compare_state(g, o, tag):
 
 
 @pytest.mark.parametrize("run", ["step_small_fp16", "step_prefill_kgs32_fp32", "step_gqa_d128_fp32",
-                                 "step_gqa_d128_fp16", "step_gqa7_d128_kgs32_fp16", "step_long_prefill_fp32"])
+                                 "step_gqa_d128_fp16", "step_gqa7_d128_kgs32_fp16", "step_long_prefill_fp32",
+                                 "step_d80_fp16", "step_d96_kgs32_fp32"])
 def test_full_steps_lockstep_with_oracle(C, oracle, run):
     cfg = engine_runs.RUNS[run]
     eng = gpu_engine(C, cfg)

@@ -315,6 +315,27 @@ def test_fused_attention_random_shapes_vs_oracle(C, oracle, case):
     assert attention_ok(err), (case, err)
 
 
+ODD_HEAD_DIMS = [(4, 2, 48, 37, 9, 16, False, "tail"), (6, 2, 80, 120, 30, 16, True, "holes"),
+                 (12, 4, 96, 300, 41, 32, False, "block"), (7, 1, 112, 0, 25, 16, True, "none"),
+                 (8, 8, 144, 19, 3, 32, True, "tail"), (10, 2, 160, 260, 17, 16, False, "holes"),
+                 (3, 3, 176, 5, 60, 16, False, "tail"), (9, 3, 192, 77, 0, 16, True, "none"),
+                 (2, 1, 208, 16, 12, 32, False, "holes"), (16, 2, 224, 40, 8, 16, True, "block"),
+                 (4, 4, 240, 33, 14, 16, False, "tail")]
+
+
+@pytest.mark.parametrize("case", ODD_HEAD_DIMS, ids=[str(c) for c in ODD_HEAD_DIMS])
+def test_fused_attention_head_dims_not_powers_of_two_vs_oracle(C, oracle, case):
+    """head_dim any multiple of 16 up to 256, as the reference accepts (48 to 240,
+    GQA 1-8, both block sizes and metadata widths): each lane's channel range of
+    the VALU kernel then starts inside a V word and can run into the next one."""
+    Hq, Hkv, D, nd, nb, kgs, fp16, mask = case
+    args = make_case(oracle, Hq, Hkv, D, nd, nb, kgs, fp16, mask, seed=1300 + D)
+    out, mw = _run_fused_gpu(C, args)
+    ro, rmw = oracle.fused_attention_decode(*args)
+    err = attention_errors(out, ro, mw, rmw)
+    assert attention_ok(err), (case, err)
+
+
 @pytest.mark.parametrize("qs,ks,vs,voff", [(16.0, 50.0, 1000.0, 3000.0), (0.05, 0.01, 1e-3, 0.0), (1.0, 1.0, 1e-7, 1.0)])
 def test_fused_attention_extreme_scales(C, oracle, qs, ks, vs, voff):
     """Q, K, V far from unit scale: the f16 operands of the matrix-core path are

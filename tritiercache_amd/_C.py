@@ -15,8 +15,8 @@ call returns, so the reference's host-side callers and tests keep working.
 Differences from the reference, all documented in the C header:
   * the zero-copy getters return ROCm tensors viewing device memory (the
     reference returns numpy arrays viewing host memory);
-  * num_q_heads must be a multiple of num_kv_heads and head_dim a power of two
-    in [16, 256] (ValueError otherwise).
+  * num_q_heads must be a multiple of num_kv_heads and head_dim a multiple of
+    16 of at most 256 (ValueError otherwise).
 """
 from __future__ import annotations
 

@@ -65,11 +65,15 @@ __device__ __forceinline__ void load_f32(const float* __restrict__ p, float (&x)
             const float4 v = *reinterpret_cast<const float4*>(p + j);
             x[j] = v.x; x[j + 1] = v.y; x[j + 2] = v.z; x[j + 3] = v.w;
         }
-    } else if constexpr (N == 2) {
-        const float2 v = *reinterpret_cast<const float2*>(p);
-        x[0] = v.x; x[1] = v.y;
+    } else if constexpr (N % 2 == 0) {
+#pragma unroll
+        for (int j = 0; j < N; j += 2) {
+            const float2 v = *reinterpret_cast<const float2*>(p + j);
+            x[j] = v.x; x[j + 1] = v.y;
+        }
     } else {
-        x[0] = p[0];
+#pragma unroll
+        for (int j = 0; j < N; ++j) x[j] = p[j];
     }
 }
 
@@ -81,11 +85,15 @@ __device__ __forceinline__ void load_u32(const int32_t* __restrict__ p, uint32_t
             const int4 v = *reinterpret_cast<const int4*>(p + j);
             x[j] = v.x; x[j + 1] = v.y; x[j + 2] = v.z; x[j + 3] = v.w;
         }
-    } else if constexpr (N == 2) {
-        const int2 v = *reinterpret_cast<const int2*>(p);
-        x[0] = v.x; x[1] = v.y;
+    } else if constexpr (N % 2 == 0) {
+#pragma unroll
+        for (int j = 0; j < N; j += 2) {
+            const int2 v = *reinterpret_cast<const int2*>(p + j);
+            x[j] = v.x; x[j + 1] = v.y;
+        }
     } else {
-        x[0] = p[0];
+#pragma unroll
+        for (int j = 0; j < N; ++j) x[j] = static_cast<uint32_t>(p[j]);
     }
 }
 
@@ -259,18 +267,27 @@ __device__ __forceinline__ void split_body(const SplitArgs& a, const int split, 
             valid[0] = id01.x != -1; valid[1] = id01.y != -1;
             valid[2] = id23.x != -1; valid[3] = id23.y != -1;
             const int qhd = D / 16;
-            const int cw = (cp * CPL) >> 4;
-            const int sh0 = ((cp * CPL) & 15) * 2;
+            // The lane's channels c0 .. c0 + CPL - 1 lie in V word c0 / 16, and
+            // in the next word too when CPL does not divide 16 (head_dim 48,
+            // 80, 96, ...; CPL <= 16, so never a third).
+            constexpr bool kOneWord = (16 % CPL) == 0;
+            const int c0 = cp * CPL;
+            const int cw = c0 >> 4;
+            const int cw1 = kOneWord ? cw : ((c0 + CPL - 1) >> 4);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int t = 4 * tg + i;  // token within the 16-token word
                 const size_t vrow = static_cast<size_t>(slot0 + i) * Hkv + kvh;
                 const uint32_t vwd = static_cast<uint32_t>(in.vp[vrow * qhd + cw]);
+                const uint32_t vwd1 = kOneWord ? vwd : static_cast<uint32_t>(in.vp[vrow * qhd + cw1]);
                 const float vsc = Meta<MetaT>::load(vs, vrow);
                 const float vze = Meta<MetaT>::load(vz, vrow);
 #pragma unroll
-                for (int j = 0; j < CPL; ++j)
-                    vx[i][j] = __builtin_fmaf(static_cast<float>((vwd >> (sh0 + 2 * j)) & 3u), vsc, vze);
+                for (int j = 0; j < CPL; ++j) {
+                    const int c = c0 + j;
+                    const uint32_t w = (kOneWord || (c >> 4) == cw) ? vwd : vwd1;
+                    vx[i][j] = __builtin_fmaf(static_cast<float>((w >> (2 * (c & 15))) & 3u), vsc, vze);
+                }
                 float kd[CPL];
 #pragma unroll
                 for (int j = 0; j < CPL; ++j)
@@ -1222,8 +1239,8 @@ int attn_check_shapes(int Hq, int Hkv, int D, int kgs) {
     if (Hq <= 0 || Hkv <= 0 || D <= 0)
         TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_q_heads, num_kv_heads, and head_dim must be positive integers.");
     if (Hq % Hkv != 0) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "num_q_heads must be a multiple of num_kv_heads.");
-    if (D % 16 != 0 || D > 256 || (D & (D - 1)) != 0)
-        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "head_dim must be one of 16, 32, 64, 128, 256.");
+    if (D % 16 != 0 || D > 256)
+        TT_FAIL(TT_ERR_INVALID_ARGUMENT, "head_dim must be a multiple of 16, at most 256.");
     if (kgs != 16 && kgs != 32) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "k_group_size must be 16 or 32.");
     return TT_OK;
 }
@@ -1366,11 +1383,22 @@ int attn_launch_split(const AttnInputs& real_in, const AttnPlan& plan, void* ws,
     }
     const dim3 grid(plan.nsplit, in.Hkv, chunks);
     if (plan.nsplit_p != 0) TT_FAIL(TT_ERR_RUNTIME, "attention plan does not match head_dim");
-    switch (in.D) {
-    case 16: return launch_split_g<1>(a, grid, gp, in.meta_fp16, stream);
-    case 32: return launch_split_g<2>(a, grid, gp, in.meta_fp16, stream);
-    case 64: return launch_split_g<4>(a, grid, gp, in.meta_fp16, stream);
-    case 128: return launch_split_g<8>(a, grid, gp, in.meta_fp16, stream);
+    switch (in.D / 16) {
+    case 1: return launch_split_g<1>(a, grid, gp, in.meta_fp16, stream);
+    case 2: return launch_split_g<2>(a, grid, gp, in.meta_fp16, stream);
+    case 3: return launch_split_g<3>(a, grid, gp, in.meta_fp16, stream);
+    case 4: return launch_split_g<4>(a, grid, gp, in.meta_fp16, stream);
+    case 5: return launch_split_g<5>(a, grid, gp, in.meta_fp16, stream);
+    case 6: return launch_split_g<6>(a, grid, gp, in.meta_fp16, stream);
+    case 7: return launch_split_g<7>(a, grid, gp, in.meta_fp16, stream);
+    case 8: return launch_split_g<8>(a, grid, gp, in.meta_fp16, stream);
+    case 9: return launch_split_g<9>(a, grid, gp, in.meta_fp16, stream);
+    case 10: return launch_split_g<10>(a, grid, gp, in.meta_fp16, stream);
+    case 11: return launch_split_g<11>(a, grid, gp, in.meta_fp16, stream);
+    case 12: return launch_split_g<12>(a, grid, gp, in.meta_fp16, stream);
+    case 13: return launch_split_g<13>(a, grid, gp, in.meta_fp16, stream);
+    case 14: return launch_split_g<14>(a, grid, gp, in.meta_fp16, stream);
+    case 15: return launch_split_g<15>(a, grid, gp, in.meta_fp16, stream);
     default: return launch_split_g<16>(a, grid, gp, in.meta_fp16, stream);
     }
 }

@@ -4,7 +4,7 @@
 // Argument validation follows the reference binding (csrc/bindings.cpp:120-128,
 // 139-147: counts non-negative, heads/dim positive, data pointers nullable
 // exactly when their count is zero) and adds the shape limits of the gfx950
-// kernels (GQA ratio integral, head_dim a power of two in [16, 256]).
+// kernels (GQA ratio integral, head_dim a multiple of 16 of at most 256).
 #include "tt_attn.h"
 
 #include <mutex>

@@ -259,15 +259,17 @@ __device__ void flush_waiting_room(const RouteArgs& a, int blocks) {
                                reinterpret_cast<uint32_t*>(a.kp) + static_cast<size_t>(blocks) * words * kvs + hc,
                                kvs);
     }
-    // V rows: one lane per packed word. The engine's head_dim is a power of
-    // two of at most 256, so D / 16 lanes form an aligned group that divides
-    // blockDim, and a row's lanes are never split between iterations.
+    // V rows: one lane per packed word, a row's D / 16 words on an aligned
+    // group of lanes padded to a power of two (head_dim a multiple of 16, at
+    // most 256: at most 16 lanes, a group that divides blockDim), so a row's
+    // lanes are never split between iterations.
     const int wpr = a.D / 16;
-    for (int th = threadIdx.x; th < a.chunk * a.H * wpr; th += blockDim.x) {
-        const int r = th / wpr, w = th % wpr;
+    const int group = quant_v_group(wpr);
+    for (int th = threadIdx.x; th < a.chunk * a.H * group; th += blockDim.x) {
+        const int r = th / group, w = th % group;
         const int t = r / a.H, h = r % a.H;
         const size_t mi = (static_cast<size_t>(blocks) * a.chunk + t) * a.H + h;
-        quant_v_row_lanes<MetaT>(a.wr_v + static_cast<size_t>(t) * kvs + static_cast<size_t>(h) * a.D, w, wpr, wpr,
+        quant_v_row_lanes<MetaT>(a.wr_v + static_cast<size_t>(t) * kvs + static_cast<size_t>(h) * a.D, w, wpr, group,
                                  vs + mi, vz + mi, a.vp + mi * wpr);
     }
     for (int t = threadIdx.x; t < a.chunk; t += blockDim.x)
