@@ -196,6 +196,7 @@ def pmc_summary(dirs):
     import collections
     import csv
     import glob
+    import re
 
     vals = collections.defaultdict(list)  # (kernel, counter) -> per-dispatch totals
     for d in dirs:
@@ -204,8 +205,10 @@ def pmc_summary(dirs):
             names = {}
             for r in csv.DictReader(open(f)):
                 k = r["Kernel_Name"]
-                kind = ("attn_packed_kernel<4, float>" if "attn_packed_kernel<4, float>" in k else
-                        "attn_packed_kernel<4, unsigned short>" if "attn_packed_kernel<4, unsigned short>" in k else
+                # attn_packed_kernel<4, float> or <4, float, false> (the unpaired instantiation)
+                kind = ("attn_packed_kernel<4, float>" if re.search(r"attn_packed_kernel<4, float(, false)?>", k) else
+                        "attn_packed_kernel<4, unsigned short>"
+                        if re.search(r"attn_packed_kernel<4, unsigned short(, false)?>", k) else
                         "copy 256 MiB (calibration)" if "copyBuffer" in k else None)
                 if kind is None:
                     continue
@@ -341,19 +344,97 @@ def engine_bench(args, torch, L, lib):
         cnt = np.zeros(23, np.int64)
         L.check(lib.tt_engine_counters(engines[0], cnt.ctypes.data, sp()), "counters")
         c = dict(zip(names, (int(x) for x in cnt)))
+        roof = engine_kernel_roofline(engines) if deferred and cfg["mode"] == "step" else None
         for h in engines:
             lib.tt_engine_destroy(h)
         torch.cuda.synchronize()
-        return us, warm, c
+        return us, warm, c, roof
+
+    def engine_kernel_roofline(engines, reps=20):
+        """The attention partials kernel over the engines' own tiers as they stand after the timed steps, with
+        the counts from each engine's counters: per layer the FP32 tiers (sinks, heavy hitters, recent window)
+        gathered into one dense array -- the rows and bytes the engine's launch reads from its three buffers --
+        and the packed store used in place. A HIP graph of the layers' partials launches, HIP events on the
+        launch stream around `reps` replays after 10 untimed ones: µs per launch, and the algorithmic bytes
+        per launch from the actual tier counts (averaged over the layers)."""
+        from tritiercache_amd._C import _DeviceView
+
+        def view(h, which, shape, typestr):
+            p, n, es = C.c_void_p(), C.c_int64(), C.c_int()
+            L.check(lib.tt_engine_buffer(h, which, C.byref(p), C.byref(n), C.byref(es), sp()), "buffer")
+            want = int(np.prod(shape))
+            assert want <= n.value, (which, shape, n.value)
+            if want == 0:
+                return None
+            return torch.as_tensor(_DeviceView(p.value, shape, typestr, None), device="cuda")
+
+        mt = "<u2" if cfg["meta"] == "fp16" else "<f4"
+        kgs, W = cfg["kgs"], cfg["kgs"] // 16
+        fp16 = 1 if cfg["meta"] == "fp16" else 0
+        layer_in, total_bytes, max_ws = [], 0, 0
+        for h in engines:
+            cnt = np.zeros(23, np.int64)
+            L.check(lib.tt_engine_counters(h, cnt.ctypes.data, sp()), "counters")
+            cc = dict(zip(names, (int(x) for x in cnt)))
+            s_, hh, rw, nb = cc["s_count"], cc["hh_count"], cc["rw_count"], cc["pbs_blocks_used"]
+            ks, vs = [], []
+            for wk, wv, n_rows in ((0, 1, s_), (4, 5, hh), (2, 3, rw)):
+                if n_rows:
+                    ks.append(view(h, wk, (n_rows, Hkv, D), "<f4"))
+                    vs.append(view(h, wv, (n_rows, Hkv, D), "<f4"))
+            nd = s_ + hh + rw
+            dK, dV = torch.cat(ks).contiguous(), torch.cat(vs).contiguous()
+            pk = (view(h, 11, (nb * W, Hkv, D), "<i4"), view(h, 12, (nb, Hkv, D), mt), view(h, 13, (nb, Hkv, D), mt),
+                  view(h, 14, (nb * kgs, Hkv, D // 16), "<i4"), view(h, 15, (nb * kgs, Hkv), mt),
+                  view(h, 16, (nb * kgs, Hkv), mt), view(h, 17, (nb * kgs,), "<i8"))
+            q = torch.randn((Hq, D), device="cuda")
+            layer_in.append((q, dK, dV, nd, pk, nb))
+            b = Hq * D * 4 + 2 * nd * Hkv * D * 4 + nb * W * Hkv * D * 4 + nb * Hkv * D * 2 * (2 if fp16 else 4) \
+                + nb * kgs * Hkv * (D // 16) * 4 + nb * kgs * Hkv * 2 * (2 if fp16 else 4) + nb * kgs * 8
+            total_bytes += b
+            max_ws = max(max_ws, int(lib.tt_fused_attention_workspace_bytes(nd, nb, Hq, Hkv, D, kgs, 1)))
+        ws = torch.empty(max_ws, dtype=torch.uint8, device="cuda")
+
+        def partials():
+            for q, dK, dV, nd, pk, nb in layer_in:
+                L.check(lib.tt_attention_partials(q.data_ptr(), dK.data_ptr(), dV.data_ptr(), nd,
+                                                  *[t.data_ptr() for t in pk], nb, Hq, Hkv, D, kgs, fp16, 1,
+                                                  ws.data_ptr(), max_ws, sp()), "partials")
+
+        partials()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            partials()
+        for _ in range(10):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us_launch = e0.elapsed_time(e1) * 1000.0 / (reps * len(layer_in))
+        bpl = total_bytes / len(layer_in)
+        del g
+        return {"bound": "hbm", "kernel": "attn_packed_kernel" if D == 128 or Hkv % 2 == 0 else "attn_split_kernel",
+                "achieved": round(bpl / (us_launch * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(bpl / (us_launch * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                "bytes_per_launch": int(bpl), "avg_launch_us": round(us_launch, 3),
+                "tiers_layer0": {"dense": layer_in[0][3], "blocks": layer_in[0][5]},
+                "how": "partials launches over the engines' own tiers after the timed steps (FP32 tiers gathered "
+                       "into one array), graph of all layers, HIP events"}
 
     deferred = cfg["mode"] == "step" and layers >= DEFER_MIN_LAYERS
     us_per_layer_calls = None
+    roof = None
     if deferred:
-        us, warm, c = run_mode(True)
-        us_per_layer_calls, _, c_ref = run_mode(False)
+        us, warm, c, roof = run_mode(True)
+        us_per_layer_calls, _, c_ref, _ = run_mode(False)
         same_state = c == c_ref
     else:
-        us, warm, c = run_mode(False)
+        us, warm, c, _ = run_mode(False)
     result = {
         "metric": f"engine decode step µs/step ({args.config})",
         "value": round(us, 2), "unit": "us/step", "n_gpus": 1, "steps": steps - warm, "warmup": warm,
@@ -377,6 +458,8 @@ def engine_bench(args, torch, L, lib):
             + nb * cfg["kgs"] * Hkv * (D // 16) * 4 + nb * cfg["kgs"] * Hkv * 2 * mb + nb * cfg["kgs"] * 8
         result["attention_bytes_per_step"] = b * layers
         result["attention_GBps"] = round(b * layers / (us * 1e-6) / 1e9, 1)
+    if roof is not None:
+        result["roofline"] = roof
     print(json.dumps(result), flush=True)
 
 
