@@ -1314,16 +1314,17 @@ AttnPlan attn_plan_impl(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int
         // The FP32 workgroups' first tiles, requested at the start, compete
         // with the packed waves' first pairs. When a packed wave has at least
         // three times the work items of an FP32 wave, the FP32 workgroups wait
-        // about twice the time the first pairs take to arrive at 5 TB/s (at
-        // most 4 us) before their first tile load; they still finish within
-        // the packed waves' time.
+        // about the time the first pairs take to arrive at 1.9 TB/s (at most
+        // 5.5 us) before their first tile load; they still finish within the
+        // packed waves' time. (At the 32k Llama-3-8B shape: 4.97 us; 3.8, 6.5
+        // and 8 us measured 2.5%, 2.5% and 10% slower per launch.)
         const long long tp = (pairs + 4LL * p.nsplit_p - 1) / (4LL * p.nsplit_p);
         const long long td = p.nsplit_d > 0 ? (dense_tiles + 4LL * p.nsplit_d - 1) / (4LL * p.nsplit_d) : 0;
         if (td > 0 && tp >= 3 * td) {
             const long long m = meta_fp16 ? 2 : 4;
             const long long pair_bytes = 2 * (512 + 256 * m / W + 512 + 32 * m + 128);
             const long long burst = std::min(pairs, 4LL * p.nsplit_p) * heads * pair_bytes;
-            p.dense_delay = static_cast<int>(std::min<long long>(400, burst / 25000));
+            p.dense_delay = static_cast<int>(std::min<long long>(550, burst / 19000));
         }
     } else {
         // One round of resident workgroups, but at least ~32 packed-tile
