@@ -402,6 +402,140 @@ __device__ __forceinline__ void dense_load(const AttnInputs& in, const DenseView
     }
 }
 
+// One 16-token FP32 tile for the VALU path of query groups of one or two
+// heads: lane (tg = lane / 16, cp = lane % 16) holds keys and values of
+// tokens 4 tg .. 4 tg + 3, channels 8 cp .. 8 cp + 7.
+struct DenseTileV {
+    float kx[4][8], vx[4][8];
+};
+
+__device__ __forceinline__ void dense_load(const AttnInputs& in, const DenseView& dv, const int kvh, const int k,
+                                           DenseTileV& t) {
+    const int lane = threadIdx.x & 63;
+    const int tg = lane >> 4, cp = lane & 15;
+    const int tok0 = 16 * k + 4 * tg;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const DenseRow r = dense_row(in, dv, kvh, tok0 + i);
+        load_f32<8>(r.k + 8 * cp, t.kx[i]);
+        load_f32<8>(r.v + 8 * cp, t.vx[i]);
+    }
+}
+
+// The FP32 tiers of the workgroup's share on the VALU, for GP <= 2. An f32
+// matrix-core tile (v_mfma_f32_16x16x4_f32, 32 cycles for 16 x 16 x 4) puts
+// one query head in each of its 16 columns, so with one or two heads it does
+// 8 or 4 times the work the VALU does for the same tile (per launch: an
+// 8k-context 32/32-head layer 18.1 against 16.7 us, a 32k 16/8-head layer
+// 15.8 against 15.1 us, head_dim-64 heads in pairs at 8k 32/32 heads 12.0
+// against 11.6 us). Same tile order, logits
+// and LDS partial layout as dense_share. Lane (tg, cp) sums its 8-channel
+// products, a DPP row sum completes the logit of token 4 tg + i; the online
+// softmax is exact (the reference moves with every tile's maximum).
+template <int GP>
+__device__ __forceinline__ void dense_share_valu(const SplitArgs& a, const DenseView& dv, const int d0,
+                                                 const int d1, const int kvh, const int g0, const int gc,
+                                                 const int wave, const float* q_l, const DenseTileV& t0,
+                                                 float* dl) {
+    static_assert(GP <= 2, "the VALU path holds every head's accumulators");
+    const AttnInputs& in = a.in;
+    const int lane = threadIdx.x & 63;
+    const int tg = lane >> 4, cp = lane & 15;
+    const int G = in.Hq / in.Hkv;
+    const int Nd = dv.Nd;
+    float m[GP], l[GP], acc[GP][8];
+#pragma unroll
+    for (int g = 0; g < GP; ++g) {
+        m[g] = kNegInf;
+        l[g] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] = 0.0f;
+    }
+    auto consume = [&](const DenseTileV& t, const int k) {
+        const int tok0 = 16 * k + 4 * tg;
+        float s[4][GP];
+#pragma unroll
+        for (int g = 0; g < GP; ++g) {
+            const float4 qa = *reinterpret_cast<const float4*>(q_l + g * kMfD + cp * 8);
+            const float4 qb = *reinterpret_cast<const float4*>(q_l + g * kMfD + cp * 8 + 4);
+            const float qg[8] = {qa.x, qa.y, qa.z, qa.w, qb.x, qb.y, qb.z, qb.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float d = 0.0f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) d = __builtin_fmaf(qg[j], t.kx[i][j], d);
+                const float v = row_sum16(d) * a.scale2;
+                s[i][g] = (tok0 + i < Nd) ? v : kNegInf;
+            }
+        }
+        if (a.logits) {
+#pragma unroll
+            for (int g = 0; g < GP; ++g) {
+                if (g < gc && cp == g) {
+                    float* lr = a.logits + static_cast<size_t>(kvh * G + g0 + g) * a.ld + tok0;
+                    if (tok0 + 4 <= Nd) {
+                        st_dev4(a.logits, static_cast<uint32_t>(in.Hq) * a.ld * 4u,
+                                static_cast<uint32_t>((lr - a.logits) * 4),
+                                make_float4(s[0][g], s[1][g], s[2][g], s[3][g]));
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            if (tok0 + i < Nd) lr[i] = s[i][g];
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < GP; ++g) {
+            const float tm = xrow_max(fmaxf(fmaxf(s[0][g], s[1][g]), fmaxf(s[2][g], s[3][g])));
+            const float mn = fmaxf(m[g], tm);
+            const float alpha = (m[g] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(m[g] - mn);
+            float p[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) p[i] = (s[i][g] == kNegInf) ? 0.0f : __builtin_amdgcn_exp2f(s[i][g] - mn);
+            l[g] = __builtin_fmaf(l[g], alpha, (p[0] + p[1]) + (p[2] + p[3]));
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                float v = acc[g][j] * alpha;
+                v = __builtin_fmaf(p[0], t.vx[0][j], v);
+                v = __builtin_fmaf(p[1], t.vx[1][j], v);
+                v = __builtin_fmaf(p[2], t.vx[2][j], v);
+                v = __builtin_fmaf(p[3], t.vx[3][j], v);
+                acc[g][j] = v;
+            }
+            m[g] = mn;
+        }
+    };
+    int kb = d0 + wave;
+    if (kb < d1) {
+        consume(t0, kb);  // in flight since the start of the kernel
+        kb += 4;
+    }
+#pragma unroll 1
+    for (int k = kb; k < d1; k += 4) {
+        DenseTileV t;
+        dense_load(in, dv, kvh, k, t);
+        consume(t, k);
+    }
+    // The four token groups share m: sum them, then the partial into LDS.
+    float* my = dl + wave * GP * (2 + kMfD);
+#pragma unroll
+    for (int g = 0; g < GP; ++g) {
+        const float lt = xrow_sum(l[g]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[g][j] = xrow_sum(acc[g][j]);
+        if (tg == 0) {
+            float* pg = my + g * (2 + kMfD);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) pg[2 + cp * 8 + j] = acc[g][j];
+            if (cp == 0) {
+                pg[0] = m[g];
+                pg[1] = lt;
+            }
+        }
+    }
+}
+
 // Component r (a constant after unrolling) of a float4, and that component
 // scaled (values, not references, so the accumulators stay in registers).
 __device__ __forceinline__ float f4_get(const float4 v, const int r) {
@@ -562,10 +696,17 @@ __device__ __forceinline__ void dense_body(const SplitArgs& a, const int dsplit,
         while (__builtin_amdgcn_s_memrealtime() - t0 < static_cast<unsigned long long>(a.dense_delay))
             __builtin_amdgcn_s_sleep(8);
     }
-    DenseTile dt;
-    if (d0 + wave < d1) dense_load(in, dv, kvh, d0 + wave, dt);
-    __syncthreads();
-    dense_share<GP>(a, dv, d0, d1, kvh, g0, gc, wave, q_l, dt, dl);
+    if constexpr (GP <= 2) {
+        DenseTileV dt;
+        if (d0 + wave < d1) dense_load(in, dv, kvh, d0 + wave, dt);
+        __syncthreads();
+        dense_share_valu<GP>(a, dv, d0, d1, kvh, g0, gc, wave, q_l, dt, dl);
+    } else {
+        DenseTile dt;
+        if (d0 + wave < d1) dense_load(in, dv, kvh, d0 + wave, dt);
+        __syncthreads();
+        dense_share<GP>(a, dv, d0, d1, kvh, g0, gc, wave, q_l, dt, dl);
+    }
     __syncthreads();
     const int split = a.nsplit_p + dsplit;
     for (int idx = threadIdx.x; idx < gc * kMfD; idx += 256) {
