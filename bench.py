@@ -57,7 +57,8 @@ CONFIGS = {
     # 256 MB Infinity Cache
     "mha-8k-8layers": (32, 32, 128, 8192, 8, None),
     "qwen2-7b-128k": (28, 4, 128, 131072, 28, "t3"),
-    # head_dim 64 (the SmolLM / TinyLlama / Qwen2-0.5B head size): the VALU split kernel, GQA 4:1
+    # head_dim 64 (the SmolLM / TinyLlama / Qwen2-0.5B head size), GQA 4:1: KV heads taken in pairs as heads of
+    # 128 channels on the matrix-core kernel
     "llama-hd64-32k": (32, 8, 64, 32768, 32, "x8"),
 }
 
@@ -623,7 +624,8 @@ def set_omp_threads(n):
         return False
 
 
-ARITHMETIC = ("f32 inputs and outputs; FP32 tiers on the VALU in f32; packed tiles on the matrix cores "
+ARITHMETIC = ("f32 inputs and outputs; FP32 tiers in f32 (on the matrix cores, v_mfma_f32_16x16x4_f32, for query "
+              "groups of four or more heads; on the VALU for one or two); packed tiles on the matrix cores "
               "(v_mfma_f32_16x16x32_f16, f32 accumulation) with exact f16 2-bit codes (V codes centred, 2q-3) and "
               "the f32 coefficients Q*k_scale and p*v_scale each split into an f16 high and low part (~22 "
               "significant bits); softmax in f32 with v_exp_f32")
