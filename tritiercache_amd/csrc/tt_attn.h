@@ -113,8 +113,10 @@ inline bool logits_fit(long long Hq, long long ld) { return Hq * ld * 4LL <= 0xF
 constexpr int kMaxBatchSeqs = 64;
 
 // Split-K plan of one batched launch over seqs[0, nseq). Every sequence gets
-// partial slots in proportion to its work (packed pairs + FP32 tiles); the
-// slots of all sequences together make one round of resident workgroups.
+// packed and FP32-tier partial slots under one cap on the work a slot
+// carries (packed pairs, or 4 units per FP32 tile); the slots of all
+// sequences together make one round of resident workgroups, the FP32-tier
+// ones a whole number of dispatch rounds after all packed ones.
 // Workspace: part_ml [slot][Hq][2] and part_acc [slot][Hq][128] in per-sequence
 // runs ([Hq][nsplit_i] each), row statistics [nseq][Hq][2], logits [Hq][ld_i]
 // per sequence that wants mean weights.
@@ -125,6 +127,11 @@ struct BatchPlan {
     int tok_base[kMaxBatchSeqs + 1] = {};   // prefix of per-sequence logits row strides
     int mean_base[kMaxBatchSeqs + 1] = {};  // prefix of per-sequence mean-weight workgroups
     int nsplit_p[kMaxBatchSeqs] = {};       // packed slots of each sequence (the rest are FP32-tier slots)
+    // Launch order: the packed slots of all sequences (prefix pk_base), then
+    // their FP32-tier slots (prefix dn_base), so that the FP32 workgroups
+    // come in whole dispatch rounds, one per CU, as for one sequence.
+    int pk_base[kMaxBatchSeqs + 1] = {};
+    int dn_base[kMaxBatchSeqs + 1] = {};
     size_t off_ml = 0, off_acc = 0, off_rowstat = 0, off_logits = 0, bytes = 0;
 };
 

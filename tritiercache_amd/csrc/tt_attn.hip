@@ -967,7 +967,8 @@ struct BatchArgs {
     int nseq, total_slots, Hq, Hkv, kgs, meta_fp16, hc, chunks;
     int slot_base[kMaxBatchSeqs + 1];
     int tok_base[kMaxBatchSeqs + 1];
-    int nsplit_p[kMaxBatchSeqs];
+    int pk_base[kMaxBatchSeqs + 1];  // launch order: packed slots of all sequences, then
+    int dn_base[kMaxBatchSeqs + 1];  // their FP32-tier slots
 };
 
 // Largest i < n with base[i] <= x (base non-decreasing, base[0] = 0 <= x).
@@ -993,8 +994,17 @@ attn_batched_kernel(const BatchArgs b) {
     const int hz = static_cast<int>(q % static_cast<unsigned>(b.hc));
     const int g = static_cast<int>((q / static_cast<unsigned>(b.hc)) * 8 + (id & 7));
     if (g >= b.total_slots) return;  // padding slot of the last group of 8
-    const int i = batch_find(b.slot_base, b.nseq, g);
-    const int s = g - b.slot_base[i];
+    // launch slot g -> (sequence i, its split s): the packed slots of all
+    // sequences first, then all FP32-tier slots
+    const int npk = b.pk_base[b.nseq];
+    int i, s;
+    if (g < npk) {
+        i = batch_find(b.pk_base, b.nseq, g);
+        s = g - b.pk_base[i];
+    } else {
+        i = batch_find(b.dn_base, b.nseq, g - npk);
+        s = (b.pk_base[i + 1] - b.pk_base[i]) + (g - npk - b.dn_base[i]);
+    }
     const tt_decode_seq& d = b.seqs[i];
     SplitArgs a;
     a.in.Q = d.Q;
@@ -1020,7 +1030,7 @@ attn_batched_kernel(const BatchArgs b) {
     a.logits = d.mean_attn_weights ? b.logits + static_cast<size_t>(b.tok_base[i]) * b.Hq : nullptr;
     a.ld = b.tok_base[i + 1] - b.tok_base[i];
     a.nsplit = b.slot_base[i + 1] - b.slot_base[i];
-    a.nsplit_p = b.nsplit_p[i];
+    a.nsplit_p = b.pk_base[i + 1] - b.pk_base[i];
     a.nsplit_d = a.nsplit - a.nsplit_p;
     a.wd = 8;
     a.wp = 1;
@@ -1521,20 +1531,78 @@ BatchPlan batch_plan(const tt_decode_seq* seqs, int nseq, int Hq, int Hkv, int D
     }
     const long long target = std::max<long long>(1, std::min<long long>(round, total / 8));
     const long long per_wg = std::max<long long>(1, (mean_blocks + kMeanMaxWgs - 1) / kMeanMaxWgs);
-    long long slot = 0, tok = 0, mean = 0;
-    for (int i = 0; i < nseq; ++i) {
-        long long n = total > 0 ? (units[i] * target + total / 2) / total : 1;
-        n = std::max<long long>(1, n);
+    // Per sequence: packed slots np[i] (at least one) and FP32-tier slots
+    // nd[i] (at most one per tile), sized to the work rather than rounded
+    // from each sequence's fraction of it (with a few slots per sequence,
+    // rounding left slots up to 40% above the mean). `cap` is the work units a
+    // slot may carry; the smallest cap whose slots fit in `budget` is found
+    // by bisection.
+    long long np[kMaxBatchSeqs], nd[kMaxBatchSeqs];
+    auto packed_slots = [&](const int i, const long long cap) {
+        return std::max<long long>(1, (units[i] - dunits[i] + cap - 1) / cap);
+    };
+    auto dense_slots = [&](const int i, const long long cap) {
         const long long dtiles = dunits[i] / kDenseTileCost;
-        long long nd = 0;
-        if (dtiles > 0) {
-            nd = (n * dunits[i] + units[i] / 2) / units[i];
-            nd = std::max<long long>(1, std::min(nd, dtiles));
+        return dtiles > 0 ? std::min(dtiles, std::max<long long>(1, (dunits[i] + cap - 1) / cap)) : 0LL;
+    };
+    auto min_cap = [&](const long long budget, auto&& slots_at) {
+        long long lo = 1, hi = 1;
+        for (int i = 0; i < nseq; ++i) hi = std::max(hi, units[i]);
+        if (slots_at(hi) > budget) return hi;  // one slot per sequence and kind is already over
+        while (lo < hi) {
+            const long long mid = lo + (hi - lo) / 2;
+            if (slots_at(mid) <= budget)
+                hi = mid;
+            else
+                lo = mid + 1;
         }
-        const long long np = std::max<long long>(1, n - nd);
+        return hi;
+    };
+    long long total_d = 0;
+    for (int i = 0; i < nseq; ++i) total_d += dunits[i];
+    const long long per_round = (res.cus % heads == 0) ? res.cus / heads : 0;  // slots of one dispatch round
+    if (per_round > 0 && res.per_cu >= 2 && total_d > 0 && total / 8 >= per_round * res.per_cu) {
+        // The device filled once, each kind in whole dispatch rounds (one
+        // workgroup per CU each), as for one sequence: every CU runs the same
+        // mix of packed and FP32-tier work. (16 sequences of 5k-32k tokens,
+        // 32/8 heads: 4.06-4.12 against 4.62-4.67 ms per 32-layer step; the
+        // per-sequence caps alone 4.47-4.55.)
+        long long rd = (res.per_cu * total_d + total / 2) / total;
+        rd = std::max<long long>(1, std::min<long long>(rd, res.per_cu - 1));
+        const long long cp = min_cap((res.per_cu - rd) * per_round, [&](const long long c) {
+            long long n = 0;
+            for (int i = 0; i < nseq; ++i) n += packed_slots(i, c);
+            return n;
+        });
+        const long long cd = min_cap(rd * per_round, [&](const long long c) {
+            long long n = 0;
+            for (int i = 0; i < nseq; ++i) n += dense_slots(i, c);
+            return n;
+        });
+        for (int i = 0; i < nseq; ++i) {
+            np[i] = packed_slots(i, cp);
+            nd[i] = dense_slots(i, cd);
+        }
+    } else {
+        const long long c = min_cap(target, [&](const long long cc) {
+            long long n = 0;
+            for (int i = 0; i < nseq; ++i) n += packed_slots(i, cc) + dense_slots(i, cc);
+            return n;
+        });
+        for (int i = 0; i < nseq; ++i) {
+            np[i] = packed_slots(i, c);
+            nd[i] = dense_slots(i, c);
+        }
+    }
+    long long slot = 0, tok = 0, mean = 0, pk = 0, dn = 0;
+    for (int i = 0; i < nseq; ++i) {
         p.slot_base[i] = static_cast<int>(slot);
-        p.nsplit_p[i] = static_cast<int>(np);
-        slot += np + nd;
+        p.nsplit_p[i] = static_cast<int>(np[i]);
+        p.pk_base[i] = static_cast<int>(pk);
+        p.dn_base[i] = static_cast<int>(dn);
+        slot += np[i] + nd[i];
+        pk += np[i];
+        dn += nd[i];
         p.tok_base[i] = static_cast<int>(tok);
         p.mean_base[i] = static_cast<int>(mean);
         if (seqs[i].mean_attn_weights) {
@@ -1543,6 +1611,8 @@ BatchPlan batch_plan(const tt_decode_seq* seqs, int nseq, int Hq, int Hkv, int D
             mean += ((tub + kMeanTokens - 1) / kMeanTokens + per_wg - 1) / per_wg;
         }
     }
+    p.pk_base[nseq] = static_cast<int>(pk);
+    p.dn_base[nseq] = static_cast<int>(dn);
     p.slot_base[nseq] = static_cast<int>(slot);
     p.tok_base[nseq] = static_cast<int>(tok);
     p.mean_base[nseq] = static_cast<int>(mean);
@@ -1583,7 +1653,8 @@ int batch_launch(const BatchPlan& plan, const tt_decode_seq* seqs_dev, int Hq, i
     b.chunks = chunks;
     std::memcpy(b.slot_base, plan.slot_base, sizeof(b.slot_base));
     std::memcpy(b.tok_base, plan.tok_base, sizeof(b.tok_base));
-    std::memcpy(b.nsplit_p, plan.nsplit_p, sizeof(b.nsplit_p));
+    std::memcpy(b.pk_base, plan.pk_base, sizeof(b.pk_base));
+    std::memcpy(b.dn_base, plan.dn_base, sizeof(b.dn_base));
     const long long wgs = static_cast<long long>((plan.total_slots + 7) / 8) * 8 * b.hc;
     if (wgs > 0x7fffffffLL) TT_FAIL(TT_ERR_INVALID_ARGUMENT, "attention grid too large");
     int rc = TT_OK;
