@@ -512,14 +512,16 @@ __device__ __forceinline__ float4 load_ml_pair(const float* p) {
 
 // Workgroups per query head in the merge. One workgroup holds the loads of
 // kMergeU splits per thread-group in flight (16384 / width splits for `width`
-// channels); a head with more splits than that is cut into slices of 32
-// channels (head_dim a multiple of 32), each merged by its own workgroup that
-// rebuilds the head's (M, L) from the split statistics, so the merge stays
-// one round trip of loads. A paired head_dim-64 head covers only its own 64
-// channels of the pair's 128.
+// channels); a head with more than 4096 / width splits (32 at head_dim 128)
+// is cut into slices of 32 channels (head_dim a multiple of 32), each merged
+// by its own workgroup that rebuilds the head's (M, L) from the split
+// statistics: the merge stays one round trip of loads, and each workgroup
+// issues a quarter of them (32k Llama-3-8B layers, 96 splits: 640.8 against
+// 650.7 us per step with f16 metadata, 656.2 against 662.7 with f32). A
+// paired head_dim-64 head covers only its own 64 channels of the pair's 128.
 __host__ __device__ inline int fin_merge_slices(const int D, const int pair_g, const int nsplit) {
     const int need = pair_g ? 64 : D;
-    if (nsplit * need <= 16 * 256 * 4 || need % 32 != 0) return 1;
+    if (nsplit * need <= 4096 || need % 32 != 0) return 1;
     return need / 32;
 }
 
