@@ -115,6 +115,20 @@ def test_batched_equals_single_sequence_calls(C, oracle):
         assert rel_err(host(e["mean_attn_weights"]), host(mw)) <= ATTN_TOL
 
 
+@pytest.mark.parametrize("fp16", [False, True])
+def test_batched_device_filling_plan_with_one_tier_sequences(C, oracle, fp16):
+    """Enough work to fill the device (packed slots of all sequences launched before all FP32-tier slots), with
+    sequences that have no FP32 tokens or no packed blocks between the others: each sequence's slots are found
+    through the packed and FP32 prefix tables, where a sequence without FP32 tokens repeats its predecessor's
+    FP32 offset."""
+    sizes = [(0, 800), (260, 400), (0, 300), (300, 0), (40, 520), (0, 1), (1000, 64)]
+    cases = _ragged(oracle, 32, 8, 128, 16, fp16, sizes, seed=1500 + fp16)
+    entries = [_entry(a) for a in cases]
+    C.fused_attention_decode_batched(entries, 32, 8, 128, 16, "fp16" if fp16 else "fp32")
+    torch.cuda.synchronize()
+    _check(oracle, cases, entries, [True] * len(cases))
+
+
 def test_batched_errors(C, oracle):
     from tritiercache_amd import _lib
 
