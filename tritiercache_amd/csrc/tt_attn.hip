@@ -1521,6 +1521,7 @@ BatchPlan batch_plan(const tt_decode_seq* seqs, int nseq, int Hq, int Hkv, int D
     // (at least ~8 units of work per slot, as for one sequence).
     const long long round = std::max<long long>(1, static_cast<long long>(res.cus) * res.per_cu / heads);
     constexpr long long kDenseTileCost = 4;
+    constexpr long long kBatchSlotUnits = 40;  // work units per slot below which another round does not pay
     long long units[kMaxBatchSeqs], dunits[kMaxBatchSeqs], total = 0, mean_blocks = 0;
     for (int i = 0; i < nseq; ++i) {
         const long long pairs = (static_cast<long long>(seqs[i].num_blocks) * W + 1) / 2;
@@ -1563,7 +1564,28 @@ BatchPlan batch_plan(const tt_decode_seq* seqs, int nseq, int Hq, int Hkv, int D
     long long total_d = 0;
     for (int i = 0; i < nseq; ++i) total_d += dunits[i];
     const long long per_round = (res.cus % heads == 0) ? res.cus / heads : 0;  // slots of one dispatch round
-    if (per_round > 0 && res.per_cu >= 2 && total_d > 0 && total / 8 >= per_round * res.per_cu) {
+    // Resident rounds of workgroups the batch's work fills at about kBatchSlotUnits units per slot (at most 3)
+    const long long rounds = std::min<long long>(3, total / (kBatchSlotUnits * round));
+    auto one_cap = [&](const long long budget) {
+        const long long c = min_cap(budget, [&](const long long cc) {
+            long long n = 0;
+            for (int i = 0; i < nseq; ++i) n += packed_slots(i, cc) + dense_slots(i, cc);
+            return n;
+        });
+        for (int i = 0; i < nseq; ++i) {
+            np[i] = packed_slots(i, c);
+            nd[i] = dense_slots(i, c);
+        }
+    };
+    if (rounds >= 2) {
+        // Several resident rounds under one cap: a slot is a fraction of a
+        // sequence, and workgroups that finish early hand their CU to the
+        // next ones, which evens out what the per-sequence slot counts cannot
+        // (16 sequences of 5k-32k tokens, 32/8 heads: 3.71-3.73 ms per step
+        // with three rounds, 3.87 with two, 4.05-4.09 with the one-round plan
+        // below, 3.91 with four).
+        one_cap(rounds * round);
+    } else if (per_round > 0 && res.per_cu >= 2 && total_d > 0 && total / 8 >= per_round * res.per_cu) {
         // The device filled once, each kind in whole dispatch rounds (one
         // workgroup per CU each), as for one sequence: every CU runs the same
         // mix of packed and FP32-tier work. (16 sequences of 5k-32k tokens,
@@ -1586,15 +1608,7 @@ BatchPlan batch_plan(const tt_decode_seq* seqs, int nseq, int Hq, int Hkv, int D
             nd[i] = dense_slots(i, cd);
         }
     } else {
-        const long long c = min_cap(target, [&](const long long cc) {
-            long long n = 0;
-            for (int i = 0; i < nseq; ++i) n += packed_slots(i, cc) + dense_slots(i, cc);
-            return n;
-        });
-        for (int i = 0; i < nseq; ++i) {
-            np[i] = packed_slots(i, c);
-            nd[i] = dense_slots(i, c);
-        }
+        one_cap(target);
     }
     long long slot = 0, tok = 0, mean = 0, pk = 0, dn = 0;
     for (int i = 0; i < nseq; ++i) {
