@@ -126,10 +126,11 @@ struct BatchPlan {
     int slot_base[kMaxBatchSeqs + 1] = {};  // prefix of per-sequence slot counts
     int tok_base[kMaxBatchSeqs + 1] = {};   // prefix of per-sequence logits row strides
     int mean_base[kMaxBatchSeqs + 1] = {};  // prefix of per-sequence mean-weight workgroups
-    int nsplit_p[kMaxBatchSeqs] = {};       // packed slots of each sequence (the rest are FP32-tier slots)
     // Launch order: the packed slots of all sequences (prefix pk_base), then
     // their FP32-tier slots (prefix dn_base), so that the FP32 workgroups
     // come in whole dispatch rounds, one per CU, as for one sequence.
+    // Sequence i's packed slots are the first pk_base[i + 1] - pk_base[i] of
+    // its slot_base run.
     int pk_base[kMaxBatchSeqs + 1] = {};
     int dn_base[kMaxBatchSeqs + 1] = {};
     size_t off_ml = 0, off_acc = 0, off_rowstat = 0, off_logits = 0, bytes = 0;

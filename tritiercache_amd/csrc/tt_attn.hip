@@ -1613,7 +1613,6 @@ BatchPlan batch_plan(const tt_decode_seq* seqs, int nseq, int Hq, int Hkv, int D
     long long slot = 0, tok = 0, mean = 0, pk = 0, dn = 0;
     for (int i = 0; i < nseq; ++i) {
         p.slot_base[i] = static_cast<int>(slot);
-        p.nsplit_p[i] = static_cast<int>(np[i]);
         p.pk_base[i] = static_cast<int>(pk);
         p.dn_base[i] = static_cast<int>(dn);
         slot += np[i] + nd[i];
