@@ -59,7 +59,7 @@ RAGGED = [(260, 40), (0, 35), (300, 0), (17, 1), (120, 130), (5, 3), (64, 64), (
 
 @pytest.mark.parametrize("Hq,Hkv,kgs,fp16", [(32, 8, 16, False), (32, 8, 16, True), (28, 4, 16, False),
                                             (16, 2, 32, False), (8, 8, 16, True), (12, 2, 16, True),
-                                            (6, 2, 16, False), (28, 4, 32, True)])
+                                            (6, 2, 16, False), (28, 4, 32, True), (16, 8, 16, False)])
 def test_batched_ragged_vs_oracle(C, oracle, Hq, Hkv, kgs, fp16):
     cases = _ragged(oracle, Hq, Hkv, 128, kgs, fp16, RAGGED, seed=1000 + Hq + kgs)
     entries = [_entry(a) for a in cases]
