@@ -60,7 +60,17 @@ CONFIGS = {
     # head_dim 64 (the SmolLM / TinyLlama / Qwen2-0.5B head size), GQA 4:1: KV heads taken in pairs as heads of
     # 128 channels on the matrix-core kernel
     "llama-hd64-32k": (32, 8, 64, 32768, 32, "x8"),
+    # head sizes on the VALU split kernel: head_dim 256 with GQA 2:1 (the Gemma-2-9B shape, 42 layers) and
+    # head_dim 80 with 32/32 heads (the Phi-2 shape, 32 layers)
+    "gemma2-9b-hd256-8k": (16, 8, 256, 8192, 42, "x8"),
+    "phi2-hd80-2k": (32, 32, 80, 2048, 32, None),
 }
+
+
+def dominant_kernel(D: int, Hkv: int) -> str:
+    """The partials kernel a layer of this shape runs: the matrix-core one for head_dim 128 and for head_dim 64 with
+    an even KV-head count (heads taken in pairs), the VALU split kernel for every other head_dim."""
+    return "attn_packed_kernel" if D == 128 or (D == 64 and Hkv % 2 == 0) else "attn_split_kernel"
 
 
 def tier_sizes(ctx: int):
@@ -419,7 +429,7 @@ def engine_bench(args, torch, L, lib):
         us_launch = e0.elapsed_time(e1) * 1000.0 / (reps * len(layer_in))
         bpl = total_bytes / len(layer_in)
         del g
-        return {"bound": "hbm", "kernel": "attn_packed_kernel" if D == 128 or Hkv % 2 == 0 else "attn_split_kernel",
+        return {"bound": "hbm", "kernel": dominant_kernel(D, Hkv),
                 "achieved": round(bpl / (us_launch * 1e-6) / 1e9, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(bpl / (us_launch * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
                 "bytes_per_launch": int(bpl), "avg_launch_us": round(us_launch, 3),
@@ -906,7 +916,7 @@ def main():
         "bytes_read_per_step": bpl * layers,
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_packed_kernel" if D == 128 or Hkv % 2 == 0 else "attn_split_kernel",
+            "kernel": dominant_kernel(D, Hkv),
             "achieved": round(kern_gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
