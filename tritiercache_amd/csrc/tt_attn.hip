@@ -1225,10 +1225,23 @@ Residency split_residency(int D, int G, int fp16, bool pair = false) {
     if (use_packed_kernel(D)) {
         fn = fp16 ? packed_kernel_ptr<uint16_t>(gp, pair) : packed_kernel_ptr<float>(gp, pair);
     } else {
-        switch (D) {
-        case 16: fn = split_kernel_ptr<1>(gp, fp16); break;
-        case 32: fn = split_kernel_ptr<2>(gp, fp16); break;
-        case 64: fn = split_kernel_ptr<4>(gp, fp16); break;
+        // the instantiation the launch runs (channels per lane = head_dim / 16)
+        switch (D / 16) {
+        case 1: fn = split_kernel_ptr<1>(gp, fp16); break;
+        case 2: fn = split_kernel_ptr<2>(gp, fp16); break;
+        case 3: fn = split_kernel_ptr<3>(gp, fp16); break;
+        case 4: fn = split_kernel_ptr<4>(gp, fp16); break;
+        case 5: fn = split_kernel_ptr<5>(gp, fp16); break;
+        case 6: fn = split_kernel_ptr<6>(gp, fp16); break;
+        case 7: fn = split_kernel_ptr<7>(gp, fp16); break;
+        case 8: fn = split_kernel_ptr<8>(gp, fp16); break;
+        case 9: fn = split_kernel_ptr<9>(gp, fp16); break;
+        case 10: fn = split_kernel_ptr<10>(gp, fp16); break;
+        case 11: fn = split_kernel_ptr<11>(gp, fp16); break;
+        case 12: fn = split_kernel_ptr<12>(gp, fp16); break;
+        case 13: fn = split_kernel_ptr<13>(gp, fp16); break;
+        case 14: fn = split_kernel_ptr<14>(gp, fp16); break;
+        case 15: fn = split_kernel_ptr<15>(gp, fp16); break;
         default: fn = split_kernel_ptr<16>(gp, fp16); break;
         }
     }
@@ -1339,16 +1352,21 @@ AttnPlan attn_plan_impl(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int
             p.dense_delay = static_cast<int>(std::min<long long>(550, burst / 19000));
         }
     } else {
-        // One round of resident workgroups, but at least ~8 packed-tile units
-        // of work per workgroup (a wave then has about two tiles): the loop
-        // is arithmetic-bound, and fewer, longer workgroups left CUs idle
-        // (at least ~32 units: head_dim 256 with 16/8 heads at 8k context
-        // 35.9 us per launch against 20.9, head_dim 80 with 32/32 heads at 2k
-        // 18.2 against 12.8).
+        // One round of resident workgroups, two when four or more fit on a
+        // CU (head_dim up to ~128 at one or two heads per group), with at
+        // least ~8 packed-tile units of work per workgroup and round: the
+        // loop is arithmetic-bound, and fewer, longer workgroups left CUs
+        // idle. Per launch: head_dim 256 with 16/8 heads at 8k context (two
+        // workgroups per CU) 20.9 us against 35.9 with ~32 units per
+        // workgroup and 24.6 with two rounds; head_dim 80 with 32/32 heads at
+        // 2k (five per CU) 11.2 against 18.2 and 12.8 (one round); head_dim 96
+        // with 32/32 heads at 4k (four per CU) 17.0 against 23.1 (one round);
+        // head_dim 64 with 12/3 heads at 8k 9.5 against 10.6 (one round).
         const long long units = dense_tiles * 8 + static_cast<long long>(blocks_ub) * W;
-        const long long cap = std::max<long long>(1, units / 8);
+        const long long rounds = res.per_cu >= 4 ? 2 : 1;
+        const long long cap = std::max<long long>(1, units * rounds / 8);
         p.nsplit_p = 0;
-        p.nsplit_d = static_cast<int>(std::max<long long>(1, std::min(per_head, cap)));
+        p.nsplit_d = static_cast<int>(std::max<long long>(1, std::min(rounds * per_head, cap)));
     }
     p.nsplit = p.nsplit_p + p.nsplit_d;
     p.token_ub = dense_ub + blocks_ub * kgs;
