@@ -1303,10 +1303,11 @@ AttnPlan attn_plan_impl(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int
     const long long per_head = std::max<long long>(1, (resident + heads - 1) / heads);
     const long long dense_tiles = (dense_ub + 15) / 16;
     if (use_packed_kernel(D)) {
-        // One resident round of workgroups per head, at least ~8 units of work
-        // each so the partials stay small (a 32-token pair of packed tiles is
-        // one unit, a 16-token FP32 tile kDenseTileCost), shared between packed
-        // and FP32 workgroups in proportion to their work.
+        // One resident round of workgroups per head, at least ~4 units of work
+        // each (~8 for the whole-round layout below) so the partials stay
+        // small (a 32-token pair of packed tiles is one unit, a 16-token FP32
+        // tile kDenseTileCost), shared between packed and FP32 workgroups in
+        // proportion to their work.
         //
         // When the launch fills the device, each kind gets whole dispatch
         // rounds (one workgroup per CU each): the kernel's workgroup order
@@ -1352,7 +1353,10 @@ AttnPlan attn_plan_impl(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int
                 const long long td = nd > 0 ? (dense_tiles + 4LL * nd - 1) / (4LL * nd) : 0;
                 return td > 0 && tp >= 3 * td;
             };
-            const long long share = std::max<long long>(1, std::min(per_head, units / 8));
+            // (short contexts: at least ~4 work units per slot; with 8, 32/8
+            // heads at 4k took 8.0 us per launch against 7.3, at 2k 7.9
+            // against 7.1, 28/4 heads at 8k 8.6 against 7.7)
+            const long long share = std::max<long long>(1, std::min(per_head, units / 4));
             long long np, nd;
             split(share >= 8 ? (share + 7) / 8 * 8 : share, np, nd);
             const long long fit = 8 * (resident / (8 * heads));
