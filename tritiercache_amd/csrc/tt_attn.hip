@@ -1304,10 +1304,11 @@ AttnPlan attn_plan_impl(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int
     const long long dense_tiles = (dense_ub + 15) / 16;
     if (use_packed_kernel(D)) {
         // One resident round of workgroups per head, at least ~4 units of work
-        // each (~8 for the whole-round layout below) so the partials stay
-        // small (a 32-token pair of packed tiles is one unit, a 16-token FP32
-        // tile kDenseTileCost), shared between packed and FP32 workgroups in
-        // proportion to their work.
+        // each so the partials stay small (a 32-token pair of packed tiles is
+        // one unit, a 16-token FP32 tile kDenseTileCost), shared between
+        // packed and FP32 workgroups in proportion to their work. (With ~8
+        // units as the bar for the whole-round layout, 32/8 heads at 8k and
+        // 12k took 8.9 and 10.3 us per launch against 8.5 and 9.9.)
         //
         // When the launch fills the device, each kind gets whole dispatch
         // rounds (one workgroup per CU each): the kernel's workgroup order
@@ -1319,7 +1320,7 @@ AttnPlan attn_plan_impl(int dense_ub, int blocks_ub, int Hq, int Hkv, int D, int
         const long long dense_units = dense_tiles * kDenseTileCost;
         const long long units = pairs + dense_units;
         const long long round = (res.cus % heads == 0) ? res.cus / heads : 0;  // slots per dispatch round
-        if (round > 0 && round % 8 == 0 && res.per_cu >= 2 && units / 8 >= round * res.per_cu) {
+        if (round > 0 && round % 8 == 0 && res.per_cu >= 2 && units / 4 >= round * res.per_cu) {
             long long rd = 0;
             if (dense_tiles > 0) {
                 rd = (res.per_cu * dense_units + units / 2) / units;
