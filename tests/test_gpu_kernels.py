@@ -459,6 +459,10 @@ def _tiered_layer(C, Hq, Hkv, D, ctx, fp16, seed, k_outliers=None):
     # more pairs than its logits buffer holds (flushes inside the loop)
     ("llama3-8b-96k", 32, 8, 98304, False, "x8"),
     ("mha-32k", 32, 32, 32768, True, None),
+    # KV head counts that do not divide the CUs into whole rounds: slot groups
+    # rounded up (40/40 at 8k) or down to what every XCD holds (40/10 at 16k)
+    ("phi3-medium-16k", 40, 10, 16384, False, "x8"),
+    ("mha40-8k", 40, 40, 8192, True, None),
     # head_dim 64: KV heads taken in pairs as heads of 128 channels on the matrix
     # cores (GQA 4:1 -> groups of 8, 1:1 -> groups of 2, 7:1 -> 14 in chunks of 8),
     # and an odd KV head count on the VALU kernel
